@@ -1,0 +1,185 @@
+"""Pin the CPU oracle (oracle/cnna_oracle.py) before trusting it.
+
+* golden vectors written by the reference itself (tests/golden/*.npz);
+* closed forms and textbook reductions a plausible mistake would break;
+* brute force on tiny inputs.
+"""
+import glob
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import cnna_oracle as O
+
+GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
+
+
+def load_case(path):
+    z = np.load(path, allow_pickle=False)
+    kw = json.loads(bytes(z["ctor"]).decode())
+    cfg = O.Config(**kw)
+    sd = {k[len("param:"):]: torch.from_numpy(z[k]) for k in z.files if k.startswith("param:")}
+    p = O.Params.from_module_state(sd, cfg.convolution_type)
+    cand = torch.from_numpy(z["cand"]) if "cand" in z.files else None
+    return cfg, p, torch.from_numpy(z["x"]), cand, torch.from_numpy(z["out"])
+
+
+def test_golden_present():
+    assert len(GOLDEN) >= 20
+
+
+@pytest.mark.parametrize("path", GOLDEN, ids=[os.path.basename(p) for p in GOLDEN])
+def test_oracle_matches_reference_golden(path):
+    cfg, p, x, cand, out = load_case(path)
+    got = O.forward(x, p, cfg, cand=cand, mode="reference")
+    tol = 1e-11 if x.dtype == torch.float64 else 2e-5
+    torch.testing.assert_close(got, out, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("path", [p for p in GOLDEN if p.endswith("_f64.npz")],
+                         ids=lambda p: os.path.basename(p))
+def test_exact_mode_matches_reference_in_f64(path):
+    cfg, p, x, cand, out = load_case(path)
+    got = O.forward(x, p, cfg, cand=cand, mode="exact")
+    torch.testing.assert_close(got, out, rtol=1e-11, atol=1e-11)
+
+
+def test_head_merge_closed_form():
+    torch.manual_seed(0)
+    for (B, H, dk, N) in [(2, 3, 4, 7), (1, 2, 5, 3), (3, 4, 2, 9)]:
+        y = torch.randn(B * H, dk, N, dtype=torch.float64)
+        torch.testing.assert_close(O.head_merge(y, B, H, N), O.head_merge_closed_form(y, B, H))
+
+
+def test_head_merge_h1_is_transpose():
+    y = torch.randn(3, 5, 7, dtype=torch.float64)
+    torch.testing.assert_close(O.head_merge(y, 3, 1, 197), y.transpose(1, 2))
+
+
+def test_head_merge_seq_length_mismatch_raises():
+    y = torch.randn(2 * 3, 4, 8)
+    with pytest.raises(RuntimeError):
+        O.head_merge(y, 2, 3, 9)
+    with pytest.raises(RuntimeError):
+        O.head_merge(torch.randn(2 * 3, 4, 16), 2, 3, 8)   # divisible but wrong
+
+
+def test_split_heads_index_formula():
+    x = torch.randn(2, 5, 6)
+    s = O.split_heads(x, 3)
+    for b in range(2):
+        for h in range(3):
+            for c in range(2):
+                for n in range(5):
+                    assert s[b * 3 + h, c, n] == x[b, n, h * 2 + c]
+
+
+def test_stable_topk_bruteforce_with_ties():
+    g = torch.Generator().manual_seed(1)
+    S = torch.randint(0, 4, (6, 5, 11), generator=g).to(torch.float64)
+    S[0, 0, 3] = float("nan")
+    for largest in (True, False):
+        vals, idx = O.stable_topk(S, 4, largest)
+        for a in range(6):
+            for b in range(5):
+                row = S[a, b].tolist()
+                def key(j):
+                    v = row[j]
+                    if math.isnan(v):
+                        return (1, 0, j)
+                    return (0, -v if largest else v, j)
+                exp = sorted(range(11), key=key)[:4]
+                assert idx[a, b].tolist() == exp
+
+
+def test_torch_topk_is_not_index_stable():
+    # the reason the oracle uses a stable sort (CPU kernel, ties)
+    v, i = torch.topk(torch.tensor([1.0, 3, 3, 2, 3, 0]), 3)
+    _, si = O.stable_topk(torch.tensor([1.0, 3, 3, 2, 3, 0]), 3, True)
+    assert si.tolist() == [1, 2, 4]
+    assert sorted(i.tolist()) == [1, 2, 4]
+
+
+def test_euclidean_is_cdist():
+    cfg = O.Config(d_hidden=8, num_heads=2, K=3, magnitude_type="euclidean")
+    k = torch.randn(4, 4, 9, dtype=torch.float64)
+    q = torch.randn(4, 4, 7, dtype=torch.float64)
+    S = O.similarity(k, q, cfg)
+    torch.testing.assert_close(S, torch.cdist(k.transpose(1, 2), q.transpose(1, 2)))
+
+
+def test_cosine_bounded_and_self_one():
+    cfg = O.Config(d_hidden=8, num_heads=2, K=3, magnitude_type="cosine")
+    k = torch.randn(4, 4, 9, dtype=torch.float64)
+    S = O.similarity(k, k, cfg)
+    assert S.abs().max() <= 1 + 1e-12
+    torch.testing.assert_close(torch.diagonal(S, dim1=1, dim2=2), torch.ones(4, 9, dtype=torch.float64))
+
+
+def test_matmul_symmetric_when_same_projection():
+    cfg = O.Config(d_hidden=8, num_heads=2, K=3)
+    k = torch.randn(4, 4, 9, dtype=torch.float64)
+    S = O.similarity(k, k, cfg)
+    torch.testing.assert_close(S, S.transpose(1, 2))
+    torch.testing.assert_close(S[0, 1, 2], (k[0, :, 1] @ k[0, :, 2]) / 2.0)
+
+
+def test_full_k_reduces_to_softmax_attention():
+    """K == Nq, unit depthwise weight, softmax: the conv sums softmax(S) * v over
+    all candidates -- textbook attention with query=k, key=q, value=v."""
+    B, N, C, H = 2, 7, 8, 2
+    cfg = O.Config(d_hidden=C, num_heads=H, K=N, seq_length=N)
+    p = O.init_params(cfg, seed=3, dtype=torch.float64)
+    x = torch.randn(B, N, C, dtype=torch.float64)
+    out, it = O.forward(x, p, cfg, mode="exact", return_intermediates=True)
+    att = F.scaled_dot_product_attention(it.k.transpose(1, 2), it.q.transpose(1, 2), it.v.transpose(1, 2))
+    torch.testing.assert_close(it.y, att.transpose(1, 2))
+
+
+def test_standard_conv_is_einsum():
+    B, N, C, H, K = 2, 6, 8, 2, 3
+    cfg = O.Config(d_hidden=C, num_heads=H, K=K, seq_length=N, convolution_type="standard")
+    p = O.init_params(cfg, seed=4, dtype=torch.float64)
+    x = torch.randn(B, N, C, dtype=torch.float64)
+    _, it = O.forward(x, p, cfg, mode="exact", return_intermediates=True)
+    g = torch.stack([it.v[b][:, it.idx[b]] for b in range(B * H)])        # (BH, c, N, K)
+    ref = torch.einsum("ocr,bcnr->bon", p.conv0, g * it.w.unsqueeze(1))
+    torch.testing.assert_close(it.y, ref)
+
+
+def test_sampled_hand_worked():
+    """N=5, Ns=3, K=3, H=1, d=2, matmul, no softmax, depthwise weight 1."""
+    cfg = O.Config(d_hidden=2, num_heads=1, K=3, sampling_type="random", num_samples=3,
+                   softmax_topk_val=False)
+    eye = torch.eye(2, dtype=torch.float64)
+    p = O.Params(eye, eye, eye, eye, torch.ones(2, 1, 3, dtype=torch.float64))
+    x = torch.tensor([[[1., 0.], [0., 1.], [2., 0.], [0., 3.], [1., 1.]]], dtype=torch.float64)
+    cand = torch.tensor([4, 0, 2])
+    out, it = O.forward(x, p, cfg, cand=cand, mode="reference", return_intermediates=True)
+    s2 = math.sqrt(2)
+    # S[i, j] = x_i . x_cand[j] / sqrt(2), then S[cand[j], j] = -0.1
+    # token 0: [1, -0.1(self), 2]/s2 -> top2 cols {2, 0} -> tokens [2, 4]
+    assert it.idx[0, 0].tolist() == [0, 2, 4]
+    torch.testing.assert_close(it.vals[0, 0], torch.tensor([1.0, 2 / s2, 1 / s2], dtype=torch.float64))
+    # token 4 (a candidate itself): [-0.1(self), 1/s2, 2/s2] -> cols {2, 1} -> tokens [2, 0]
+    assert it.idx[0, 4].tolist() == [4, 2, 0]
+    y0 = 1.0 * x[0, 0] + (2 / s2) * x[0, 2] + (1 / s2) * x[0, 4]
+    torch.testing.assert_close(out[0, 0], y0)
+
+
+def test_spatial_indices_are_1d_linspace():
+    cfg = O.Config(d_hidden=192, num_heads=3, K=9, sampling_type="spatial", num_samples=8)
+    assert O.sample_indices(cfg, 197).tolist() == [0, 28, 56, 84, 112, 140, 168, 196]
+
+
+def test_gradcheck_oracle_f64():
+    B, N, C, H = 1, 6, 4, 2
+    cfg = O.Config(d_hidden=C, num_heads=H, K=3, seq_length=N, convolution_type="standard")
+    p = O.init_params(cfg, seed=5, dtype=torch.float64)
+    x = torch.randn(B, N, C, dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda t: O.forward(t, p, cfg, mode="exact"), (x,))
