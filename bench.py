@@ -1,0 +1,193 @@
+"""Benchmark: ConvNN-Attention layer throughput on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3]
+
+One step = one forward of ``MultiHeadConvNNAttention`` (eval mode) over one
+batch of synthetic input already resident in HBM.  The default workload is
+B=32, N=1024, C=384, H=3, K=9, bf16, matmul similarity,
+depthwise conv, sampling 'all'.  Prints one JSON line with tokens/s, the
+roofline of the dominant kernel (timed with HIP events on the launch stream)
+and the CPU baseline (the oracle's restatement of the reference op sequence
+on a bounded sample, timed on this host's cores).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "convolutional-nearest-neighbor-attention_amd")
+sys.path.insert(0, ROOT)
+sys.path.insert(0, PKG)
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_F32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    # name: (B, N, C, H, K, dtype, metric, conv, sampling, num_samples, seed)
+    "c3": (32, 1024, 384, 3, 9, torch.bfloat16, "matmul", "depthwise", "all", -1, 1),
+    "c2layer": (128, 197, 192, 3, 9, torch.bfloat16, "matmul", "depthwise", "all", -1, 0),
+    "c1": (64, 65, 192, 3, 9, torch.float32, "cosine", "depthwise", "all", -1, 0),
+    "c4a": (128, 197, 192, 3, 9, torch.float32, "matmul", "depthwise", "random", 64, 2),
+    "c4b": (128, 197, 192, 3, 9, torch.float32, "matmul", "depthwise", "spatial", 8, 2),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-sample-batch", type=int, default=8)
+    return ap.parse_args()
+
+
+def flops_of(B, N, Nq, C, H, K, conv):
+    dk = C // H
+    proj = 2 * B * C * C * (3 * N + Nq)
+    sim = 2 * B * N * Nq * C
+    cv = {"depthwise": 2 * B * N * C * K, "standard": 2 * B * N * C * dk * K,
+          "depthwise-separable": 2 * B * N * C * (K + dk)}[conv]
+    return proj, sim, cv
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU figures are not part of it",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import cnna_ops as ops
+    from layers import MultiHeadConvNNAttention
+
+    B, N, C, H, K, dtype, metric, conv, sampling, ns, seed = CONFIGS[args.config]
+    dev = "cuda"
+    torch.manual_seed(seed)
+    m = MultiHeadConvNNAttention(C, H, 0.0, K, sampling, ns, 0, metric, seq_length=N,
+                                 convolution_type=conv).to(dev).to(dtype).eval()
+    x = torch.randn(B, N, C, device=dev).to(dtype)
+    Nq = N if sampling == "all" else ns
+
+    # ---- whole-layer timing
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            m(x)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            m(x)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / args.steps
+    tokens = B * N
+    value = tokens / (ms / 1e3)
+
+    # ---- per-stage timing with HIP events on the launch stream
+    cand = m._candidates(x)
+    d = ops.make_desc(B, N, C, H, Nq, K, N, dtype, metric, conv, True, cand is not None, False)
+    w0, w1 = m._conv_weights()
+    Wq, Wk, Wv, Wo = m.W_q.weight, m.W_k.weight, m.W_v.weight, m.W_o.weight
+    stages = {"project": [], "select": [], "aggregate": [], "output_proj": []}
+    with torch.no_grad():
+        for it in range(args.warmup + args.steps):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+            ev[0].record()
+            q, k, v, qn, kn = ops.project_qkv(d, x, cand, Wq, Wk, Wv)
+            ev[1].record()
+            idx, vals = ops.select(d, k, q, kn, qn, cand)
+            ev[2].record()
+            y = ops.aggregate(d, v, idx, vals, w0, w1)
+            ev[3].record()
+            ops.output_proj(d, y, Wo)
+            ev[4].record()
+            if it >= args.warmup:
+                torch.cuda.synchronize()
+                for i, name in enumerate(stages):
+                    stages[name].append(ev[i].elapsed_time(ev[i + 1]))
+    st_ms = {k_: sorted(v_)[len(v_) // 2] for k_, v_ in stages.items()}
+
+    proj_f, sim_f, conv_f = flops_of(B, N, Nq, C, H, K, conv)
+    es = 2 if dtype == torch.bfloat16 else 4
+    peak_mfma = PEAK_BF16_TFLOPS if dtype == torch.bfloat16 else PEAK_F32_TFLOPS
+    # algorithmic work per launch of each stage
+    work = {
+        "project": ("mfma", 2 * B * C * C * (2 * N + Nq)),
+        "select": ("mfma", sim_f),
+        # read V, write y, read int32 index + fp32 value per neighbour
+        "aggregate": ("hbm", 2 * B * N * C * es + B * H * N * K * 8),
+        "output_proj": ("mfma", 2 * B * N * C * C),
+    }
+    dom = max(st_ms, key=st_ms.get)
+    bound, amount = work[dom]
+    t_s = st_ms[dom] / 1e3
+    if bound == "mfma":
+        achieved = amount / t_s / 1e12
+        roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": peak_mfma,
+                "unit": "TFLOP/s", "frac": round(achieved / peak_mfma, 4), "traffic": None}
+    else:
+        achieved = amount / t_s / 1e9
+        roof = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None}
+
+    total_flops = proj_f + sim_f + conv_f
+    layer_tflops = total_flops / (ms / 1e3) / 1e12
+
+    # ---- CPU baseline: the oracle's reference-mode op sequence on a bounded sample
+    cpu = None
+    if not args.no_cpu:
+        from oracle import cnna_oracle as O
+        ncores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(ncores)
+        bs = max(1, min(args.cpu_sample_batch, B))
+        cfg = O.Config(d_hidden=C, num_heads=H, K=K, sampling_type=sampling, num_samples=ns,
+                       magnitude_type=metric, seq_length=N, convolution_type=conv)
+        p = O.Params.from_module_state({k_: v_.detach().cpu() for k_, v_ in m.state_dict().items()}, conv)
+        xc = x[:bs].cpu()
+        cdt = dtype
+        try:
+            O.forward(xc[:1], p, cfg, cand=None if cand is None else cand.cpu().long(), mode="reference")
+        except RuntimeError:
+            cdt = torch.float32
+        xc, p = xc.to(cdt), p.to(dtype=cdt)
+        cc = None if cand is None else cand.cpu().long()
+        O.forward(xc, p, cfg, cand=cc, mode="reference")          # warm-up
+        reps, t_cpu = 0, 0.0
+        while reps < 3 or (t_cpu < 10.0 and reps < 20):
+            c0 = time.perf_counter()
+            O.forward(xc, p, cfg, cand=cc, mode="reference")
+            t_cpu += time.perf_counter() - c0
+            reps += 1
+        cpu = {"value": round(bs * N * reps / t_cpu, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+               "kind": "port",
+               "sample": f"{reps} forwards of {bs} of {B} sequences (N={N}) in "
+                         f"{str(cdt).replace('torch.', '')}, oracle reference-mode op sequence",
+               "affinity_cores": ncores, "os_cpu_count": os.cpu_count(), "torch": torch.__version__}
+
+    rec = {
+        "metric": "ConvNN-Attn layer tokens/s (N=1024,C=384,K=9,bf16); % MFMA/HBM roofline",
+        "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if dtype == torch.bfloat16 else "f32",
+        "data": "synthetic: x ~ N(0,1), random-init weights (seeded)",
+        "config": {"workload": f"{args.config}: MultiHeadConvNNAttention forward B={B} N={N} C={C} "
+                               f"H={H} K={K} {metric} {conv} sampling={sampling}",
+                   "B": B, "N": N, "C": C, "H": H, "K": K, "sampling": sampling},
+        "roofline": roof,
+        "layer": {"flops": total_flops, "tflops": round(layer_tflops, 2),
+                  "frac_of_mfma_peak": round(layer_tflops / peak_mfma, 4)},
+        "stages_ms": {k_: round(v_, 4) for k_, v_ in st_ms.items()},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,208 @@
+"""ctypes binding of libcnna.so and the autograd functions of the operator.
+
+The library is loaded from this directory; importing this module fails loudly
+when it is missing (there is no CPU or eager-PyTorch fallback).  Launches go
+on ``torch.cuda.current_stream()``; outputs and workspaces are allocated by
+PyTorch's caching allocator and handed to the C-ABI as raw pointers.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from typing import Optional
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libcnna.so")
+
+CNNA_F32, CNNA_BF16 = 0, 1
+METRICS = {"matmul": 0, "cosine": 1, "euclidean": 2}
+CONVS = {"standard": 0, "depthwise": 1, "depthwise-separable": 2}
+
+ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_OPTION, ERR_K_RANGE, ERR_SEQ, ERR_WS, ERR_GROUPS = (
+    -1, -2, -3, -4, -5, -6, -7, -8)
+
+
+class Desc(ctypes.Structure):
+    """Mirror of ``cnna_desc`` in include/cnna.h."""
+
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "B", "N", "C", "H", "Nq", "K", "seq_length", "dtype", "metric", "conv",
+        "softmax", "sampled", "coord")]
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"libcnna.so not found at {LIB_PATH}; build it with "
+            "`python convolutional-nearest-neighbor-attention_amd/build.py` (hipcc, gfx950)")
+    lib = ctypes.CDLL(LIB_PATH)
+    P, I64, I32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    D = ctypes.POINTER(Desc)
+    sigs = {
+        "cnna_abi_version": ([], I32),
+        "cnna_error_string": ([I32], ctypes.c_char_p),
+        "cnna_check_desc": ([D], I32),
+        "cnna_head_stride": ([D], I32),
+        "cnna_project_qkv": ([D, P, I64, P, P, P, P, P, P, P, P, P, P], I32),
+        "cnna_select": ([D, P, P, P, P, P, P, P, P], I32),
+        "cnna_aggregate": ([D, P, P, P, P, P, P, P], I32),
+        "cnna_output_proj": ([D, P, P, P, I64, P], I32),
+        "cnna_forward_workspace": ([D], ctypes.c_size_t),
+        "cnna_forward": ([D, P, I64, P, P, P, P, P, P, P, P, I64, P, ctypes.c_size_t, P], I32),
+    }
+    for name, (args, res) in sigs.items():
+        f = getattr(lib, name)
+        f.argtypes = args
+        f.restype = res
+    return lib
+
+
+LIB = _load()
+EXPORTED = ("cnna_abi_version", "cnna_error_string", "cnna_check_desc", "cnna_head_stride",
+            "cnna_project_qkv", "cnna_select", "cnna_aggregate", "cnna_output_proj",
+            "cnna_forward_workspace", "cnna_forward")
+
+
+def check(status: int) -> None:
+    """Map a C-ABI status to the exception type the reference raises."""
+    if status == 0:
+        return
+    msg = LIB.cnna_error_string(status).decode()
+    if status in (ERR_K_RANGE, ERR_SEQ):
+        raise RuntimeError(msg)
+    if status in (ERR_GROUPS, ERR_OPTION):
+        raise ValueError(msg)
+    if status in (ERR_DTYPE,):
+        raise TypeError(msg)
+    raise RuntimeError(msg)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return CNNA_F32
+    if dt == torch.bfloat16:
+        return CNNA_BF16
+    raise TypeError(f"cnna: unsupported dtype {dt} (float32 or bfloat16)")
+
+
+def make_desc(B, N, C, H, Nq, K, seq_length, dtype, metric, conv, softmax, sampled, coord) -> Desc:
+    d = Desc(B, N, C, H, Nq, K, seq_length, dtype_code(dtype), METRICS[metric], CONVS[conv],
+             int(bool(softmax)), int(bool(sampled)), int(bool(coord)))
+    check(LIB.cnna_check_desc(ctypes.byref(d)))
+    return d
+
+
+def head_stride(d: Desc) -> int:
+    return LIB.cnna_head_stride(ctypes.byref(d))
+
+
+# --------------------------------------------------------------------------
+# stage wrappers (each allocates its outputs with torch, launches, no sync)
+# --------------------------------------------------------------------------
+
+def project_qkv(d: Desc, x: torch.Tensor, cand: Optional[torch.Tensor], Wq, Wk, Wv):
+    """Returns q (BH,Nq,dkp), k, v (BH,N,dkp), qn, kn (euclidean norms or None)."""
+    if x.stride(2) != 1 or x.stride(0) != x.shape[1] * x.stride(1):
+        x = x.contiguous()
+    ldx = x.stride(1)
+    BH, dkp = d.B * d.H, head_stride(d)
+    q = torch.empty((BH, d.Nq, dkp), dtype=x.dtype, device=x.device)
+    k = torch.empty((BH, d.N, dkp), dtype=x.dtype, device=x.device)
+    v = torch.empty((BH, d.N, dkp), dtype=x.dtype, device=x.device)
+    qn = kn = None
+    if d.metric == METRICS["euclidean"]:
+        qn = torch.empty((BH * d.Nq,), dtype=torch.float32, device=x.device)
+        kn = torch.empty((BH * d.N,), dtype=torch.float32, device=x.device)
+    check(LIB.cnna_project_qkv(ctypes.byref(d), _ptr(x), ldx, _ptr(cand), _ptr(Wq.contiguous()),
+                               _ptr(Wk.contiguous()), _ptr(Wv.contiguous()), _ptr(q), _ptr(k),
+                               _ptr(v), _ptr(qn), _ptr(kn), _stream()))
+    return q, k, v, qn, kn
+
+
+def select(d: Desc, k, q, kn=None, qn=None, cand=None):
+    """Fused similarity + top-k: idx int32 (BH,N,K), vals fp32 (BH,N,K)."""
+    BH = d.B * d.H
+    idx = torch.empty((BH, d.N, d.K), dtype=torch.int32, device=k.device)
+    vals = torch.empty((BH, d.N, d.K), dtype=torch.float32, device=k.device)
+    check(LIB.cnna_select(ctypes.byref(d), _ptr(k), _ptr(q), _ptr(kn), _ptr(qn), _ptr(cand),
+                          _ptr(idx), _ptr(vals), _stream()))
+    return idx, vals
+
+
+def aggregate(d: Desc, v, idx, vals, w0, w1=None):
+    """Weights + gather + conv: y (BH, N, d_k) token-major."""
+    BH, dk = d.B * d.H, d.C // d.H
+    y = torch.empty((BH, d.N, dk), dtype=v.dtype, device=v.device)
+    w0 = w0.to(v.dtype).contiguous()
+    w1 = None if w1 is None else w1.to(v.dtype).contiguous()
+    check(LIB.cnna_aggregate(ctypes.byref(d), _ptr(v), _ptr(idx), _ptr(vals), _ptr(w0), _ptr(w1),
+                             _ptr(y), _stream()))
+    return y
+
+
+def output_proj(d: Desc, y, Wo):
+    """Head merge (the reference's reshape mixing) fused into out = merge(y) @ Wo^T."""
+    out = torch.empty((d.B, d.N, d.C), dtype=y.dtype, device=y.device)
+    check(LIB.cnna_output_proj(ctypes.byref(d), _ptr(y.contiguous()), _ptr(Wo.contiguous()),
+                               _ptr(out), d.C, _stream()))
+    return out
+
+
+def forward_fused(d: Desc, x, cand, Wq, Wk, Wv, Wo, w0, w1=None):
+    """Whole forward through the single ``cnna_forward`` entry point."""
+    x = x.contiguous()
+    ws_bytes = LIB.cnna_forward_workspace(ctypes.byref(d))
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=x.device)
+    out = torch.empty((d.B, d.N, d.C), dtype=x.dtype, device=x.device)
+    w0 = w0.to(x.dtype).contiguous()
+    w1 = None if w1 is None else w1.to(x.dtype).contiguous()
+    check(LIB.cnna_forward(ctypes.byref(d), _ptr(x), x.stride(1), _ptr(cand), _ptr(Wq.contiguous()),
+                           _ptr(Wk.contiguous()), _ptr(Wv.contiguous()), _ptr(Wo.contiguous()),
+                           _ptr(w0), _ptr(w1), _ptr(out), d.C, _ptr(ws), ws_bytes, _stream()))
+    return out
+
+
+# --------------------------------------------------------------------------
+# autograd
+# --------------------------------------------------------------------------
+
+class ConvNNCore(torch.autograd.Function):
+    """x -> y (BH, N, d_k): projections, neighbour selection, aggregation."""
+
+    @staticmethod
+    def forward(ctx, x, Wq, Wk, Wv, w0, w1, cand, d):
+        q, k, v, qn, kn = project_qkv(d, x, cand, Wq, Wk, Wv)
+        idx, vals = select(d, k, q, kn, qn, cand)
+        y = aggregate(d, v, idx, vals, w0, w1)
+        ctx.d = d
+        ctx.save_for_backward(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, idx, vals)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        raise NotImplementedError("cnna: backward kernels are not built yet")
+
+
+class HeadMergeProj(torch.autograd.Function):
+    """y (BH, N, d_k) -> out (B, N, C) = merge(y) @ Wo^T."""
+
+    @staticmethod
+    def forward(ctx, y, Wo, d):
+        ctx.d = d
+        ctx.save_for_backward(y, Wo)
+        return output_proj(d, y, Wo)
+
+    @staticmethod
+    def backward(ctx, dout):
+        raise NotImplementedError("cnna: backward kernels are not built yet")

@@ -1,0 +1,257 @@
+// C-ABI entry points of libcnna.so (declared in include/cnna.h).
+// Validation mirrors the exceptions the reference raises (layers.py:149,
+// 251, 310, 344/365 via torch.topk, Conv1d groups check) so callers can map
+// status codes to the same Python exception types before any launch.
+#include <math.h>
+#include <string.h>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+int elem_size(int dtype) { return dtype == CNNA_BF16 ? 2 : (dtype == CNNA_F32 ? 4 : 0); }
+
+int din_of(const cnna_desc* d) { return d->C / d->H + (d->coord ? 1 : 0); }
+
+int dkp_of(const cnna_desc* d) {
+  // channels padded to the MFMA reduction depth (16) and 16-byte rows
+  return (int)cnna_round_up((size_t)din_of(d), 16);
+}
+
+int ksel_of(const cnna_desc* d) { return d->sampled ? d->K - 1 : d->K; }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int cnna_abi_version(void) { return CNNA_ABI_VERSION; }
+
+const char* cnna_error_string(int code) {
+  switch (code) {
+    case CNNA_OK: return "ok";
+    case CNNA_ERR_NULL: return "cnna: required pointer is NULL";
+    case CNNA_ERR_SHAPE: return "cnna: inconsistent or unsupported shape";
+    case CNNA_ERR_DTYPE: return "cnna: unsupported dtype (float32 or bfloat16)";
+    case CNNA_ERR_OPTION: return "cnna: unknown magnitude_type / convolution_type / option combination";
+    case CNNA_ERR_K_RANGE: return "cnna: selected index k out of range";
+    case CNNA_ERR_SEQ_LENGTH: return "cnna: seq_length must equal the number of tokens when num_heads > 1";
+    case CNNA_ERR_WORKSPACE: return "cnna: workspace too small";
+    case CNNA_ERR_GROUPS: return "cnna: out_channels must be divisible by groups";
+    default: break;
+  }
+  if (code > 0) return hipGetErrorString((hipError_t)code);
+  return "cnna: unknown error";
+}
+
+int cnna_check_desc(const cnna_desc* d) {
+  if (d == nullptr) return CNNA_ERR_NULL;
+  if (d->dtype != CNNA_F32 && d->dtype != CNNA_BF16) return CNNA_ERR_DTYPE;
+  if (d->B <= 0 || d->N <= 0 || d->C <= 0 || d->H <= 0 || d->C % d->H != 0) return CNNA_ERR_SHAPE;
+  if (d->metric < CNNA_MATMUL || d->metric > CNNA_EUCLIDEAN) return CNNA_ERR_OPTION;
+  if (d->conv < CNNA_CONV_STANDARD || d->conv > CNNA_CONV_DWSEP) return CNNA_ERR_OPTION;
+  if (d->conv == CNNA_CONV_DEPTHWISE && d->coord) return CNNA_ERR_GROUPS;
+  if (d->K < 1) return CNNA_ERR_K_RANGE;
+  if (d->Nq < 0 || (!d->sampled && d->Nq != d->N)) return CNNA_ERR_SHAPE;
+  if (ksel_of(d) > d->Nq) return CNNA_ERR_K_RANGE;
+  if (ksel_of(d) > 32 || d->K > 32) return CNNA_ERR_K_RANGE;
+  if (d->H > 1 && d->seq_length != d->N) return CNNA_ERR_SEQ_LENGTH;
+  const int dkp = dkp_of(d);
+  if (d->dtype == CNNA_BF16 && dkp > 256) return CNNA_ERR_SHAPE;
+  if (d->dtype == CNNA_F32 && dkp > 128) return CNNA_ERR_SHAPE;
+  return CNNA_OK;
+}
+
+int cnna_head_stride(const cnna_desc* d) { return d ? dkp_of(d) : 0; }
+
+int cnna_project_qkv(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* cand,
+                     const void* Wq, const void* Wk, const void* Wv, void* q, void* k, void* v,
+                     float* qn, float* kn, void* stream) {
+  int st = cnna_check_desc(d);
+  if (st) return st;
+  if (!x || !Wq || !Wk || !Wv || !q || !k || !v) return CNNA_ERR_NULL;
+  if (d->sampled && !cand) return CNNA_ERR_NULL;
+  if (d->metric == CNNA_EUCLIDEAN && (!qn || !kn)) return CNNA_ERR_NULL;
+  if (ldx < d->C) return CNNA_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  const int es = elem_size(d->dtype), dk = d->C / d->H, dkp = dkp_of(d);
+  const int BH = d->B * d->H;
+
+  GemmArgs g;
+  memset(&g, 0, sizeof(g));
+  g.Kd = d->C;
+  g.a = x;
+  g.lda = ldx;
+  g.ncol_each = d->C;
+  g.o_H = d->H;
+  g.o_dk = dk;
+  g.o_dkp = dkp;
+  g.avec = ((ldx * es) % 16 == 0) && aligned16(x);
+  g.bvec = ((d->C * es) % 16 == 0) && aligned16(Wq) && aligned16(Wk) && aligned16(Wv);
+  if (!d->sampled) {
+    // one launch: [Q | K | V] = x @ [Wq; Wk; Wv]^T
+    g.M = d->B * d->N;
+    g.Nc = 3 * d->C;
+    g.w[0] = Wq; g.w[1] = Wk; g.w[2] = Wv;
+    g.o[0] = q; g.o[1] = k; g.o[2] = v;
+    g.o_rows = d->N;
+    if ((st = launch_gemm(d->dtype, GEMM_A_ROWS, GEMM_O_HEADSPLIT, g, s))) return st;
+  } else {
+    g.M = d->B * d->N;
+    g.Nc = 2 * d->C;
+    g.w[0] = Wk; g.w[1] = Wv;
+    g.o[0] = k; g.o[1] = v;
+    g.o_rows = d->N;
+    if ((st = launch_gemm(d->dtype, GEMM_A_ROWS, GEMM_O_HEADSPLIT, g, s))) return st;
+    // Q on the sampled tokens x[:, cand, :] (layers.py:285-286, 298-299)
+    g.M = d->B * d->Nq;
+    g.Nc = d->C;
+    g.w[0] = Wq; g.o[0] = q;
+    g.arow = cand;
+    g.a_rows = d->Nq;
+    g.a_src_rows = d->N;
+    g.o_rows = d->Nq;
+    if (d->Nq > 0 && (st = launch_gemm(d->dtype, GEMM_A_ROWS, GEMM_O_HEADSPLIT, g, s))) return st;
+  }
+  // coordinate channel / padding / cosine normalisation / euclidean norms
+  const bool pad = dkp != dk;
+  const bool cos = d->metric == CNNA_COSINE, euc = d->metric == CNNA_EUCLIDEAN;
+  PrepArgs p;
+  memset(&p, 0, sizeof(p));
+  p.dk = dk;
+  p.dkp = dkp;
+  p.coord = d->coord;
+  if (pad || cos || euc) {
+    p.t = k; p.rows = d->N; p.rows_total = BH * d->N; p.normalize = cos; p.norms = euc ? kn : nullptr;
+    if ((st = launch_prep(d->dtype, p, s))) return st;
+    p.t = q; p.rows = d->Nq; p.rows_total = BH * d->Nq; p.normalize = cos; p.norms = euc ? qn : nullptr;
+    if ((st = launch_prep(d->dtype, p, s))) return st;
+  }
+  if (pad) {
+    p.t = v; p.rows = d->N; p.rows_total = BH * d->N; p.normalize = 0; p.norms = nullptr;
+    if ((st = launch_prep(d->dtype, p, s))) return st;
+  }
+  return CNNA_OK;
+}
+
+int cnna_select(const cnna_desc* d, const void* k, const void* q, const float* kn, const float* qn,
+                const int32_t* cand, int32_t* idx, float* vals, void* stream) {
+  int st = cnna_check_desc(d);
+  if (st) return st;
+  if (!k || !q || !idx || !vals) return CNNA_ERR_NULL;
+  if (d->sampled && !cand) return CNNA_ERR_NULL;
+  if (d->metric == CNNA_EUCLIDEAN && (!kn || !qn)) return CNNA_ERR_NULL;
+  if (!aligned16(k) || !aligned16(q)) return CNNA_ERR_SHAPE;
+  SelArgs a;
+  memset(&a, 0, sizeof(a));
+  a.k = k; a.q = q; a.kn = kn; a.qn = qn; a.cand = d->sampled ? cand : nullptr;
+  a.idx = idx; a.vals = vals;
+  a.BH = d->B * d->H; a.N = d->N; a.Nq = d->Nq; a.dkp = dkp_of(d);
+  a.K = d->K; a.Ksel = ksel_of(d);
+  a.rb_per_bh = (d->N + 127) / 128;
+  const int dk = d->C / d->H;
+  // matmul: S = k.q / d_k**0.5 (layers.py:324); cosine inputs are normalised
+  a.kscale = (d->metric == CNNA_MATMUL) ? (float)(1.0 / sqrt((double)dk)) : 1.0f;
+  if (d->metric == CNNA_EUCLIDEAN) {
+    a.mask_val = 1.1f;                         // INF (layers.py:234)
+    a.mask_key = -(a.mask_val * a.mask_val);
+  } else {
+    a.mask_val = -0.1f;                        // NEG_INF (layers.py:235)
+    a.mask_key = a.mask_val;
+  }
+  return launch_select(d->dtype, d->metric == CNNA_EUCLIDEAN, d->sampled, a, (hipStream_t)stream);
+}
+
+int cnna_aggregate(const cnna_desc* d, const void* v, const int32_t* idx, const float* vals,
+                   const void* conv_w0, const void* conv_w1, void* y, void* stream) {
+  int st = cnna_check_desc(d);
+  if (st) return st;
+  if (!v || !idx || !vals || !conv_w0 || !y) return CNNA_ERR_NULL;
+  if (d->conv == CNNA_CONV_DWSEP && !conv_w1) return CNNA_ERR_NULL;
+  AggArgs a;
+  memset(&a, 0, sizeof(a));
+  a.v = v; a.idx = idx; a.vals = vals; a.w0 = conv_w0; a.w1 = conv_w1; a.y = y;
+  a.BH = d->B * d->H; a.N = d->N; a.K = d->K;
+  a.din = din_of(d); a.dout = d->C / d->H; a.dkp = dkp_of(d);
+  a.softmax = d->softmax; a.maximum = d->metric != CNNA_EUCLIDEAN; a.conv = d->conv;
+  return launch_aggregate(d->dtype, a, (hipStream_t)stream);
+}
+
+int cnna_output_proj(const cnna_desc* d, const void* y, const void* Wo, void* out, int64_t ldo,
+                     void* stream) {
+  int st = cnna_check_desc(d);
+  if (st) return st;
+  if (!y || !Wo || !out) return CNNA_ERR_NULL;
+  if (ldo < d->C) return CNNA_ERR_SHAPE;
+  const int es = elem_size(d->dtype);
+  GemmArgs g;
+  memset(&g, 0, sizeof(g));
+  g.M = d->B * d->N;
+  g.Nc = d->C;
+  g.Kd = d->C;
+  g.a = y;
+  g.lda = d->C;
+  g.w[0] = Wo;
+  g.ncol_each = d->C;
+  g.o[0] = out;
+  g.ldo = ldo;
+  g.bvec = ((d->C * es) % 16 == 0) && aligned16(Wo);
+  if (d->H == 1) {
+    // H == 1: merge is a plain transpose back to (B, N, C) (layers.py:248-249, 255-256)
+    g.avec = ((d->C * es) % 16 == 0) && aligned16(y);
+    return launch_gemm(d->dtype, GEMM_A_ROWS, GEMM_O_PLAIN, g, (hipStream_t)stream);
+  }
+  g.mix_N = d->N;
+  g.mix_H = d->H;
+  g.mix_dk = d->C / d->H;
+  return launch_gemm(d->dtype, GEMM_A_MIXED, GEMM_O_PLAIN, g, (hipStream_t)stream);
+}
+
+size_t cnna_forward_workspace(const cnna_desc* d) {
+  if (cnna_check_desc(d)) return 0;
+  const size_t es = elem_size(d->dtype), dkp = dkp_of(d), BH = (size_t)d->B * d->H;
+  const size_t dk = d->C / d->H;
+  size_t n = 0;
+  n += cnna_round_up(BH * d->Nq * dkp * es, 256);         // q
+  n += 2 * cnna_round_up(BH * d->N * dkp * es, 256);      // k, v
+  n += cnna_round_up(BH * d->Nq * 4, 256);                // qn
+  n += cnna_round_up(BH * d->N * 4, 256);                 // kn
+  n += 2 * cnna_round_up(BH * d->N * d->K * 4, 256);      // idx, vals
+  n += cnna_round_up(BH * d->N * dk * es, 256);           // y
+  return n;
+}
+
+int cnna_forward(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* cand, const void* Wq,
+                 const void* Wk, const void* Wv, const void* Wo, const void* conv_w0,
+                 const void* conv_w1, void* out, int64_t ldo, void* ws, size_t ws_bytes,
+                 void* stream) {
+  int st = cnna_check_desc(d);
+  if (st) return st;
+  if (!ws) return CNNA_ERR_NULL;
+  if (ws_bytes < cnna_forward_workspace(d)) return CNNA_ERR_WORKSPACE;
+  if (!aligned16(ws)) return CNNA_ERR_SHAPE;
+  const size_t es = elem_size(d->dtype), dkp = dkp_of(d), BH = (size_t)d->B * d->H;
+  const size_t dk = d->C / d->H;
+  char* p = static_cast<char*>(ws);
+  auto take = [&](size_t bytes) { void* r = p; p += cnna_round_up(bytes, 256); return r; };
+  void* q = take(BH * d->Nq * dkp * es);
+  void* k = take(BH * d->N * dkp * es);
+  void* v = take(BH * d->N * dkp * es);
+  float* qn = static_cast<float*>(take(BH * d->Nq * 4));
+  float* kn = static_cast<float*>(take(BH * d->N * 4));
+  int32_t* idx = static_cast<int32_t*>(take(BH * d->N * d->K * 4));
+  float* vals = static_cast<float*>(take(BH * d->N * d->K * 4));
+  void* y = take(BH * d->N * dk * es);
+  const bool euc = d->metric == CNNA_EUCLIDEAN;
+  if ((st = cnna_project_qkv(d, x, ldx, cand, Wq, Wk, Wv, q, k, v, euc ? qn : nullptr,
+                             euc ? kn : nullptr, stream)))
+    return st;
+  if ((st = cnna_select(d, k, q, euc ? kn : nullptr, euc ? qn : nullptr, cand, idx, vals, stream)))
+    return st;
+  if ((st = cnna_aggregate(d, v, idx, vals, conv_w0, conv_w1, y, stream))) return st;
+  return cnna_output_proj(d, y, Wo, out, ldo, stream);
+}
+
+}  // extern "C"

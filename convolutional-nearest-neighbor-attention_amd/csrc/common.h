@@ -1,0 +1,92 @@
+// Shared device helpers for the ConvNN-Attention HIP library (gfx950 only).
+//
+// Storage types: float for fp32 tensors, uint16_t holding the bf16 bit
+// pattern for bf16 tensors.  All arithmetic is fp32; bf16 is rounded to
+// nearest-even when stored, the same rounding torch applies.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+
+#include "../../include/cnna.h"
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint16_t bf16_t;
+
+#define CNNA_DEV __device__ __forceinline__
+
+CNNA_DEV float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+CNNA_DEV uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+CNNA_DEV float ldf(const float* p) { return *p; }
+CNNA_DEV float ldf(const uint16_t* p) { return bf2f(*p); }
+CNNA_DEV void stf(float* p, float v) { *p = v; }
+CNNA_DEV void stf(uint16_t* p, float v) { *p = f2bf(v); }
+
+// Smallest float strictly greater than x (x not NaN).
+CNNA_DEV float next_up(float x) {
+  if (x == INFINITY) return x;
+  if (x == 0.0f) return __uint_as_float(1u);
+  uint32_t u = __float_as_uint(x);
+  u = (x > 0.0f) ? u + 1u : u - 1u;
+  return __uint_as_float(u);
+}
+
+// MFMA 32x32 traits.  Operand layout of v_mfma_f32_32x32x{16_bf16,2_f32}:
+//   A (32 x KC): lane l supplies A[l % 32][(l / 32) * KL + 0..KL-1]
+//   B (KC x 32): lane l supplies B[(l / 32) * KL + 0..KL-1][l % 32]
+//   D (32 x 32): lane l, register v holds D[(v/4)*8 + (l/32)*4 + v%4][l % 32]
+template <typename T> struct Mfma;
+
+template <> struct Mfma<uint16_t> {
+  static constexpr int KC = 16;   // reduction depth of one instruction
+  static constexpr int KL = 8;    // elements per lane
+  typedef bf16x8_t frag;
+  static CNNA_DEV frag load(const uint16_t* p) {
+    uint4 u = *reinterpret_cast<const uint4*>(p);
+    return __builtin_bit_cast(frag, u);
+  }
+  static CNNA_DEV frag zero() { return __builtin_bit_cast(frag, make_uint4(0, 0, 0, 0)); }
+  static CNNA_DEV f32x16_t mma(frag a, frag b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma<float> {
+  static constexpr int KC = 2;
+  static constexpr int KL = 1;
+  typedef float frag;
+  static CNNA_DEV frag load(const float* p) { return *p; }
+  static CNNA_DEV frag zero() { return 0.0f; }
+  static CNNA_DEV f32x16_t mma(frag a, frag b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+};
+
+CNNA_DEV int mfma_row(int v, int lane) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
+
+// Map a linear block id so that consecutive work items land on the same XCD
+// (blocks are dealt to the 8 XCDs round-robin; each XCD has its own L2).
+CNNA_DEV int xcd_swizzle(int L, int total) {
+  if ((total & 7) != 0) return L;
+  const int per = total >> 3;
+  return (L & 7) * per + (L >> 3);
+}
+
+// torch.linspace(start, end, steps) in float32 (symmetric evaluation).
+CNNA_DEV float linspace_f32(float start, float end, int steps, int i) {
+  if (steps == 1) return start;
+  const float step = (end - start) / (float)(steps - 1);
+  const int halfway = steps / 2;
+  return (i < halfway) ? start + step * (float)i : end - step * (float)(steps - i - 1);
+}
+
+inline size_t cnna_round_up(size_t a, size_t b) { return (a + b - 1) / b * b; }

@@ -1,0 +1,127 @@
+/* C-ABI of the MI355X (gfx950) ConvNN-Attention library, libcnna.so.
+ *
+ * The reference operator is the Python class MultiHeadConvNNAttention
+ * (layers.py:132-450 of mingikang31/Convolutional-Nearest-Neighbor-Attention);
+ * it has no FFI of its own.  Each entry point below replaces one stage of its
+ * forward (layers.py:261-321) or the autograd backward of those stages.
+ *
+ * Conventions
+ *  - Every pointer is device memory owned by the caller; the library never
+ *    allocates or frees device memory and never synchronises the stream.
+ *  - `stream` is a hipStream_t passed as void* (NULL = default stream).
+ *  - Return value: 0 ok; negative = invalid argument (cnna_error_string);
+ *    positive = hipError_t of a failed launch.
+ *  - Tensors are row-major.  "Head-split" tensors are (B*H, rows, dkp):
+ *    token-major per head, dkp = cnna_head_stride(desc) channels of which the
+ *    first d_k (+1 with coordinate encoding) are used and the rest are zero.
+ *  - idx is int32 token indices (B*H, N, K); vals is fp32 (B*H, N, K) holding
+ *    the selected similarity values (for sampled paths slot 0 is the token
+ *    itself with value 1.0, layers.py:369-376).
+ */
+#ifndef CNNA_H
+#define CNNA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CNNA_ABI_VERSION 1
+
+enum cnna_dtype { CNNA_F32 = 0, CNNA_BF16 = 1 };
+/* magnitude_type (layers.py:167-168, 323-340) */
+enum cnna_metric { CNNA_MATMUL = 0, CNNA_COSINE = 1, CNNA_EUCLIDEAN = 2 };
+/* convolution_type (layers.py:186-228) */
+enum cnna_conv { CNNA_CONV_STANDARD = 0, CNNA_CONV_DEPTHWISE = 1, CNNA_CONV_DWSEP = 2 };
+
+enum cnna_status {
+  CNNA_OK = 0,
+  CNNA_ERR_NULL = -1,         /* required pointer is NULL */
+  CNNA_ERR_SHAPE = -2,        /* inconsistent or unsupported sizes */
+  CNNA_ERR_DTYPE = -3,        /* unknown dtype */
+  CNNA_ERR_OPTION = -4,       /* unknown metric / conv / option combination */
+  CNNA_ERR_K_RANGE = -5,      /* K larger than the candidates (torch.topk RuntimeError) */
+  CNNA_ERR_SEQ_LENGTH = -6,   /* seq_length != N with num_heads > 1 (layers.py:251) */
+  CNNA_ERR_WORKSPACE = -7,    /* workspace too small */
+  CNNA_ERR_GROUPS = -8        /* depthwise with coordinate encoding (Conv1d ValueError) */
+};
+
+/* Operator configuration: the constructor arguments of layers.py:133-146
+ * plus the call's shapes. */
+typedef struct cnna_desc {
+  int32_t B;            /* batch */
+  int32_t N;            /* tokens (x.shape[1]) */
+  int32_t C;            /* d_hidden */
+  int32_t H;            /* num_heads */
+  int32_t Nq;           /* candidates: N for sampling 'all', num_samples otherwise */
+  int32_t K;            /* neighbours per token (self included for sampled paths) */
+  int32_t seq_length;   /* constructor seq_length; must equal N when H > 1 */
+  int32_t dtype;        /* enum cnna_dtype */
+  int32_t metric;       /* enum cnna_metric */
+  int32_t conv;         /* enum cnna_conv */
+  int32_t softmax;      /* softmax_topk_val */
+  int32_t sampled;      /* 1 for 'random' / 'spatial' (layers.py:283-307) */
+  int32_t coord;        /* coordinate_encoding (layers.py:269-270, 439-450) */
+} cnna_desc;
+
+int cnna_abi_version(void);
+const char* cnna_error_string(int code);
+
+/* Validate a descriptor (the checks the reference performs at construction
+ * and call time, layers.py:149, 251, 310, 344/365, Conv1d groups). */
+int cnna_check_desc(const cnna_desc* d);
+
+/* Channel stride dkp of head-split tensors for this descriptor. */
+int cnna_head_stride(const cnna_desc* d);
+
+/* Q/K/V projections + head split (layers.py:264-265, 274, 286, 299 and
+ * split_head/batch_combine layers.py:237-245), plus coordinate channel and
+ * cosine normalisation / euclidean squared norms (layers.py:327-340, 439-450).
+ *   x    (B, N, C) with row stride ldx elements (channels contiguous)
+ *   cand (Nq) int32 sampled token indices, NULL for 'all'
+ *   W*   (C, C) nn.Linear weights [out, in]
+ *   q    (B*H, Nq, dkp); k, v (B*H, N, dkp)
+ *   qn, kn  fp32 squared norms (B*H*Nq), (B*H*N): euclidean only, else NULL */
+int cnna_project_qkv(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* cand,
+                     const void* Wq, const void* Wk, const void* Wv,
+                     void* q, void* k, void* v, float* qn, float* kn, void* stream);
+
+/* Fused similarity + streaming top-k (layers.py:323-340 then torch.topk in
+ * _prime/_prime_softmax/_prime_N/_prime_softmax_N, layers.py:344, 363, 391,
+ * 410, with the sampled self mask layers.py:291-292, 304-305).  The N x Nq
+ * similarity matrix is never written.  Ties break by lowest candidate index. */
+int cnna_select(const cnna_desc* d, const void* k, const void* q, const float* kn, const float* qn,
+                const int32_t* cand, int32_t* idx, float* vals, void* stream);
+
+/* Neighbour weights (softmax / raw / euclidean division), V gather and the
+ * Conv1d(kernel=K, stride=K) over the neighbours (layers.py:346-358,
+ * 378-386, 393-405, 425-436, 313).
+ *   conv_w0: standard (d_k, d_in, K) / depthwise (d_k, 1, K) / dw part (d_in, 1, K)
+ *   conv_w1: pointwise (d_k, d_in, 1) for depthwise-separable, else NULL
+ *   y (B*H, N, d_k) token-major conv output, dtype of the descriptor */
+int cnna_aggregate(const cnna_desc* d, const void* v, const int32_t* idx, const float* vals,
+                   const void* conv_w0, const void* conv_w1, void* y, void* stream);
+
+/* Head merge (layers.py:316-317, 247-259) fused into the A-operand load of
+ * the output projection W_o (layers.py:320):  out = merge(y) @ Wo^T.
+ *   out (B, N, C) with row stride ldo elements */
+int cnna_output_proj(const cnna_desc* d, const void* y, const void* Wo, void* out, int64_t ldo,
+                     void* stream);
+
+/* Bytes of workspace cnna_forward needs for this descriptor. */
+size_t cnna_forward_workspace(const cnna_desc* d);
+
+/* Whole forward of MultiHeadConvNNAttention in eval mode (dropout identity):
+ * the four stages above on one stream, intermediates in `ws`. */
+int cnna_forward(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* cand,
+                 const void* Wq, const void* Wk, const void* Wv, const void* Wo,
+                 const void* conv_w0, const void* conv_w1, void* out, int64_t ldo,
+                 void* ws, size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CNNA_H */

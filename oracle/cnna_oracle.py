@@ -440,17 +440,23 @@ def prime_dtype(v: torch.Tensor, w: torch.Tensor):
 # --------------------------------------------------------------------------
 
 def topk_exact(k_tok: torch.Tensor, q_tok: torch.Tensor, cfg: Config,
-               cand: Optional[torch.Tensor] = None, kvalid: Optional[int] = None):
+               cand: Optional[torch.Tensor] = None, kvalid: Optional[int] = None,
+               normalized_inputs: bool = False):
     """Top-k of the similarity between token-major k (BH,N,c) and q (BH,Nq,c),
     computed in float64 from the given (already rounded) operands.
 
     Returns (idx int64 (BH,N,K), vals float64 (BH,N,K), S float64 (BH,N,Nq)).
     ``kvalid`` limits the channels used (padding channels are ignored).
+    ``normalized_inputs``: cosine operands were already normalised (and rounded)
+    by the projection stage, so S is their plain dot product.
     """
     c = kvalid if kvalid is not None else k_tok.shape[-1]
     k = k_tok[..., :c].to(torch.float64).transpose(1, 2)
     q = q_tok[..., :c].to(torch.float64).transpose(1, 2)
-    S = similarity(k, q, cfg)
+    if normalized_inputs and cfg.magnitude_type == "cosine":
+        S = torch.matmul(k.transpose(1, 2), q)
+    else:
+        S = similarity(k, q, cfg)
     if cand is not None:
         S = mask_self(S, cand, cfg)
     idx, vals = select_neighbours(S, cfg, cand)

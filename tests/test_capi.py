@@ -1,0 +1,123 @@
+"""Host-side checks of the C-ABI library (no GPU needed).
+
+* libcnna.so loads and exports every entry point include/cnna.h declares;
+* descriptor validation returns the error codes that map to the exceptions the
+  reference raises (layers.py:149, 251, 310, torch.topk range, Conv1d groups).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import cnna_ops as ops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    txt = open(os.path.join(ROOT, "include", "cnna.h")).read()
+    return sorted(set(re.findall(r"\b(cnna_[a-z_0-9]+)\s*\(", txt)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_symbols()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(ops.LIB, n), n
+    assert set(names) == set(ops.EXPORTED)
+
+
+def test_abi_version():
+    assert ops.LIB.cnna_abi_version() == 1
+
+
+def desc(**kw):
+    base = dict(B=2, N=16, C=12, H=3, Nq=16, K=4, seq_length=16, dtype=ops.CNNA_F32, metric=0, conv=1,
+                softmax=1, sampled=0, coord=0)
+    base.update(kw)
+    return ops.Desc(*[base[f] for f, _ in ops.Desc._fields_])
+
+
+def status(**kw):
+    d = desc(**kw)
+    return ops.LIB.cnna_check_desc(ctypes.byref(d))
+
+
+def test_check_desc_ok():
+    assert status() == 0
+    assert status(sampled=1, Nq=5, K=6) == 0
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=7), ops.ERR_DTYPE),
+    (dict(C=13), ops.ERR_SHAPE),                       # d_hidden % num_heads
+    (dict(metric=5), ops.ERR_OPTION),
+    (dict(conv=9), ops.ERR_OPTION),
+    (dict(coord=1), ops.ERR_GROUPS),                   # depthwise + coordinate encoding
+    (dict(K=17), ops.ERR_K_RANGE),                     # K > candidates
+    (dict(sampled=1, Nq=4, K=6), ops.ERR_K_RANGE),     # K-1 > num_samples
+    (dict(seq_length=197), ops.ERR_SEQ),               # H > 1 and seq_length != N
+    (dict(K=0), ops.ERR_K_RANGE),
+])
+def test_check_desc_errors(kw, code):
+    assert status(**kw) == code
+
+
+def test_h1_ignores_seq_length():
+    assert status(H=1, seq_length=197) == 0
+
+
+def test_error_strings_and_exception_types():
+    with pytest.raises(RuntimeError):
+        ops.check(ops.ERR_K_RANGE)
+    with pytest.raises(RuntimeError):
+        ops.check(ops.ERR_SEQ)
+    with pytest.raises(ValueError):
+        ops.check(ops.ERR_GROUPS)
+    with pytest.raises(TypeError):
+        ops.check(ops.ERR_DTYPE)
+    assert b"workspace" in ops.LIB.cnna_error_string(ops.ERR_WS)
+
+
+def test_head_stride_padding():
+    d = desc(C=384, H=3, N=8, Nq=8, seq_length=8)
+    assert ops.LIB.cnna_head_stride(ctypes.byref(d)) == 128
+    d = desc(C=12, H=3)
+    assert ops.LIB.cnna_head_stride(ctypes.byref(d)) == 16
+    d = desc(C=128, H=2, conv=0, coord=1)
+    assert ops.LIB.cnna_head_stride(ctypes.byref(d)) == 80
+
+
+def test_workspace_size_positive():
+    d = desc()
+    assert ops.LIB.cnna_forward_workspace(ctypes.byref(d)) > 0
+    bad = desc(K=99)
+    assert ops.LIB.cnna_forward_workspace(ctypes.byref(bad)) == 0
+
+
+def test_module_rejects_cpu_tensors():
+    from layers import MultiHeadConvNNAttention
+    m = MultiHeadConvNNAttention(12, 3, 0.0, 4, "all", -1, 0, "matmul", seq_length=16)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        m(torch.randn(2, 16, 12))
+
+
+def test_module_matches_reference_parameter_names_and_init():
+    """Same parameter names/shapes and the same seeded initial values as the
+    oracle's restatement of the reference init order."""
+    from layers import MultiHeadConvNNAttention
+    from oracle import cnna_oracle as O
+    for conv in ("standard", "depthwise", "depthwise-separable"):
+        torch.manual_seed(0)
+        m = MultiHeadConvNNAttention(12, 3, 0.1, 4, "all", -1, 0, "matmul", seq_length=16,
+                                     convolution_type=conv)
+        names = sorted(m.state_dict().keys())
+        exp = ["W_k.weight", "W_o.weight", "W_q.weight", "W_v.weight"]
+        exp += ["conv.0.weight", "conv.1.weight"] if conv == "depthwise-separable" else ["conv.weight"]
+        assert names == sorted(exp)
+        p = O.Params.from_module_state(m.state_dict(), conv)
+        assert p.W_q.shape == (12, 12)
+        if conv == "depthwise":
+            assert torch.all(p.conv0 == 1.0) and p.conv0.shape == (4, 1, 4)
