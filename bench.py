@@ -102,11 +102,11 @@ def main():
             ev[0].record()
             q, k, v, qn, kn = ops.project_qkv(d, x, cand, Wq, Wk, Wv)
             ev[1].record()
-            idx, vals = ops.select(d, k, q, kn, qn, cand)
+            idx, vals, w = ops.select(d, k, q, kn, qn, cand)
             ev[2].record()
-            y = ops.aggregate(d, v, idx, vals, w0, w1)
+            z = ops.aggregate(d, v, idx, w, w0, w1)
             ev[3].record()
-            ops.output_proj(d, y, Wo)
+            ops.output_proj(d, z, Wo)
             ev[4].record()
             if it >= args.warmup:
                 torch.cuda.synchronize()

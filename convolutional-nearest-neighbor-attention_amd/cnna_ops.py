@@ -47,8 +47,9 @@ def _load():
         "cnna_check_desc": ([D], I32),
         "cnna_head_stride": ([D], I32),
         "cnna_project_qkv": ([D, P, I64, P, P, P, P, P, P, P, P, P, P], I32),
-        "cnna_select": ([D, P, P, P, P, P, P, P, P], I32),
-        "cnna_aggregate": ([D, P, P, P, P, P, P, P], I32),
+        "cnna_select": ([D, P, P, P, P, P, P, P, P, P], I32),
+        "cnna_aggregate_workspace": ([D], ctypes.c_size_t),
+        "cnna_aggregate": ([D, P, P, P, P, P, P, P, ctypes.c_size_t, P], I32),
         "cnna_output_proj": ([D, P, P, P, I64, P], I32),
         "cnna_forward_workspace": ([D], ctypes.c_size_t),
         "cnna_forward": ([D, P, I64, P, P, P, P, P, P, P, P, I64, P, ctypes.c_size_t, P], I32),
@@ -62,7 +63,8 @@ def _load():
 
 LIB = _load()
 EXPORTED = ("cnna_abi_version", "cnna_error_string", "cnna_check_desc", "cnna_head_stride",
-            "cnna_project_qkv", "cnna_select", "cnna_aggregate", "cnna_output_proj",
+            "cnna_project_qkv", "cnna_select", "cnna_aggregate_workspace", "cnna_aggregate",
+            "cnna_output_proj",
             "cnna_forward_workspace", "cnna_forward")
 
 
@@ -131,30 +133,32 @@ def project_qkv(d: Desc, x: torch.Tensor, cand: Optional[torch.Tensor], Wq, Wk, 
 
 
 def select(d: Desc, k, q, kn=None, qn=None, cand=None):
-    """Fused similarity + top-k: idx int32 (BH,N,K), vals fp32 (BH,N,K)."""
+    """Fused similarity + top-k: idx int32, vals fp32, neighbour weights fp32, all (BH,N,K)."""
     BH = d.B * d.H
     idx = torch.empty((BH, d.N, d.K), dtype=torch.int32, device=k.device)
     vals = torch.empty((BH, d.N, d.K), dtype=torch.float32, device=k.device)
+    w = torch.empty((BH, d.N, d.K), dtype=torch.float32, device=k.device)
     check(LIB.cnna_select(ctypes.byref(d), _ptr(k), _ptr(q), _ptr(kn), _ptr(qn), _ptr(cand),
-                          _ptr(idx), _ptr(vals), _stream()))
-    return idx, vals
+                          _ptr(idx), _ptr(vals), _ptr(w), _stream()))
+    return idx, vals, w
 
 
-def aggregate(d: Desc, v, idx, vals, w0, w1=None):
-    """Weights + gather + conv: y (BH, N, d_k) token-major."""
-    BH, dk = d.B * d.H, d.C // d.H
-    y = torch.empty((BH, d.N, dk), dtype=v.dtype, device=v.device)
+def aggregate(d: Desc, v, idx, w, w0, w1=None):
+    """Gather + conv + head merge: z (B, N, C), the tensor that enters W_o."""
+    z = torch.empty((d.B, d.N, d.C), dtype=v.dtype, device=v.device)
     w0 = w0.to(v.dtype).contiguous()
     w1 = None if w1 is None else w1.to(v.dtype).contiguous()
-    check(LIB.cnna_aggregate(ctypes.byref(d), _ptr(v), _ptr(idx), _ptr(vals), _ptr(w0), _ptr(w1),
-                             _ptr(y), _stream()))
-    return y
+    nws = LIB.cnna_aggregate_workspace(ctypes.byref(d))
+    ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=v.device) if nws else None
+    check(LIB.cnna_aggregate(ctypes.byref(d), _ptr(v), _ptr(idx), _ptr(w), _ptr(w0), _ptr(w1),
+                             _ptr(z), _ptr(ws), nws, _stream()))
+    return z
 
 
-def output_proj(d: Desc, y, Wo):
-    """Head merge (the reference's reshape mixing) fused into out = merge(y) @ Wo^T."""
-    out = torch.empty((d.B, d.N, d.C), dtype=y.dtype, device=y.device)
-    check(LIB.cnna_output_proj(ctypes.byref(d), _ptr(y.contiguous()), _ptr(Wo.contiguous()),
+def output_proj(d: Desc, z, Wo):
+    """out = z @ Wo^T (z already carries the reference's head-merge mixing)."""
+    out = torch.empty((d.B, d.N, d.C), dtype=z.dtype, device=z.device)
+    check(LIB.cnna_output_proj(ctypes.byref(d), _ptr(z.contiguous()), _ptr(Wo.contiguous()),
                                _ptr(out), d.C, _stream()))
     return out
 
@@ -178,30 +182,30 @@ def forward_fused(d: Desc, x, cand, Wq, Wk, Wv, Wo, w0, w1=None):
 # --------------------------------------------------------------------------
 
 class ConvNNCore(torch.autograd.Function):
-    """x -> y (BH, N, d_k): projections, neighbour selection, aggregation."""
+    """x -> z (B, N, C): projections, neighbour selection, aggregation, head merge."""
 
     @staticmethod
     def forward(ctx, x, Wq, Wk, Wv, w0, w1, cand, d):
         q, k, v, qn, kn = project_qkv(d, x, cand, Wq, Wk, Wv)
-        idx, vals = select(d, k, q, kn, qn, cand)
-        y = aggregate(d, v, idx, vals, w0, w1)
+        idx, vals, w = select(d, k, q, kn, qn, cand)
+        z = aggregate(d, v, idx, w, w0, w1)
         ctx.d = d
-        ctx.save_for_backward(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, idx, vals)
-        return y
+        ctx.save_for_backward(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, idx, vals, w)
+        return z
 
     @staticmethod
-    def backward(ctx, dy):
+    def backward(ctx, dz):
         raise NotImplementedError("cnna: backward kernels are not built yet")
 
 
-class HeadMergeProj(torch.autograd.Function):
-    """y (BH, N, d_k) -> out (B, N, C) = merge(y) @ Wo^T."""
+class OutputProj(torch.autograd.Function):
+    """out = z @ Wo^T."""
 
     @staticmethod
-    def forward(ctx, y, Wo, d):
+    def forward(ctx, z, Wo, d):
         ctx.d = d
-        ctx.save_for_backward(y, Wo)
-        return output_proj(d, y, Wo)
+        ctx.save_for_backward(z, Wo)
+        return output_proj(d, z, Wo)
 
     @staticmethod
     def backward(ctx, dout):

@@ -1,133 +1,191 @@
-// Neighbour weights + V gather + Conv1d(kernel=K, stride=K) over the K
-// gathered neighbours (layers.py:342-437 and self.conv at layers.py:313).
+// Neighbour aggregation (layers.py:342-437 and self.conv at layers.py:313)
+// and the reference head merge (layers.py:316-317, 247-259).
 //
-// Weights per token i (layers.py:352-355, 382-385, 394-397, 426-429):
-//   softmax_topk_val: softmax(vals) (cosine/matmul) or softmax(-vals) (euclidean)
-//   otherwise:        vals (cosine/matmul) or 1 / (vals + 1e-8) (euclidean)
-// and prime[c, i, r] = w[i, r] * v[c, idx[i, r]] is never materialised.
+//  * agg_kernel<T, VW, COPY=false>: depthwise Conv1d(kernel=K, stride=K) over
+//    the K gathered neighbours,  y[i, c] = sum_r W0[c, r] * w[i, r] * v[idx[i, r], c],
+//    where w are the neighbour weights written by the select kernel.  prime
+//    (layers.py:348-358, 402-405) is never materialised.
+//  * agg_kernel<T, VW, COPY=true>: the head merge of an already computed
+//    token-major y (standard / depthwise-separable conv paths).
 //
-// Output y is token-major (B*H, N, d_k); the head merge is applied by the
-// output projection's A-operand loader.
+// Both write either the plain token-major tensor (B*H, N, dout) or the merged
+// tensor Z (B, N, C) that enters W_o.  For H > 1 the merge mixes tokens:
+//   Z[b, t, h*dk + a] = y_bh[f] with f = a*N + t, y_bh flat token-major.
+// A block owns TI consecutive tokens of one (b, h), i.e. the flat range
+// f in [i0*dk, (i0+TI)*dk); it stages that range in LDS as rows a of length N
+// and writes each Z row's run of consecutive columns a with adjacent lanes.
+//
+// Lanes: a token is handled by LPT lanes, VW channels each (16-byte vectors).
 #include "common.h"
 #include "kernels.h"
 
 namespace {
 
-constexpr int KCAP = 32;
-
-CNNA_DEV void weights(const AggArgs& a, int64_t g, float (&w)[KCAP], int (&ix)[KCAP]) {
-  const float* vals = a.vals + g * a.K;
-  const int32_t* idx = a.idx + g * a.K;
-  float mx = -INFINITY;
+template <typename T, int VW> struct Vec;
+template <> struct Vec<uint16_t, 8> {
+  static CNNA_DEV void load(const uint16_t* p, float (&o)[8]) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-  for (int r = 0; r < KCAP; ++r) {
-    if (r < a.K) {
-      const float v = vals[r];
-      ix[r] = idx[r];
-      w[r] = (a.softmax && !a.maximum) ? -v : v;
-      mx = fmaxf(mx, w[r]);
-    } else {
-      w[r] = 0.0f;
-      ix[r] = 0;
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
     }
   }
-  if (a.softmax) {
-    float s = 0.0f;
+  static CNNA_DEV void store(uint16_t* p, const float (&o)[8]) {
+    u32x4_t w;
 #pragma unroll
-    for (int r = 0; r < KCAP; ++r)
-      if (r < a.K) {
-        w[r] = expf(w[r] - mx);
-        s += w[r];
-      }
-#pragma unroll
-    for (int r = 0; r < KCAP; ++r)
-      if (r < a.K) w[r] = w[r] / s;
-  } else if (!a.maximum) {
-#pragma unroll
-    for (int r = 0; r < KCAP; ++r)
-      if (r < a.K) w[r] = 1.0f / (w[r] + 1e-8f);
+    for (int i = 0; i < 4; ++i) w[i] = f2bf2(o[2 * i], o[2 * i + 1]);
+    *reinterpret_cast<u32x4_t*>(p) = w;
   }
-}
+};
+template <> struct Vec<float, 4> {
+  static CNNA_DEV void load(const float* p, float (&o)[4]) {
+    const float4 u = *reinterpret_cast<const float4*>(p);
+    o[0] = u.x; o[1] = u.y; o[2] = u.z; o[3] = u.w;
+  }
+  static CNNA_DEV void store(float* p, const float (&o)[4]) {
+    *reinterpret_cast<float4*>(p) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+};
+template <typename T> struct Vec<T, 1> {
+  static CNNA_DEV void load(const T* p, float (&o)[1]) { o[0] = ldf(p); }
+  static CNNA_DEV void store(T* p, const float (&o)[1]) { stf(p, o[0]); }
+};
 
-// depthwise: one wave per token, lanes over channels
-template <typename T>
-__global__ __launch_bounds__(256) void agg_dw_kernel(AggArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (g >= (int64_t)a.BH * a.N) return;
-  const int64_t bh = g / a.N;
-  float w[KCAP];
-  int ix[KCAP];
-  weights(a, g, w, ix);
-  const T* V = static_cast<const T*>(a.v) + bh * a.N * a.dkp;
-  const T* W0 = static_cast<const T*>(a.w0);
-  T* y = static_cast<T*>(a.y) + g * a.dout;
-  for (int c = lane; c < a.dout; c += 64) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int r = 0; r < KCAP; ++r)
-      if (r < a.K) acc += ldf(W0 + c * a.K + r) * (w[r] * ldf(V + (int64_t)ix[r] * a.dkp + c));
-    stf(y + c, acc);
-  }
-}
+template <typename T, int VW, bool COPY>
+__global__ __launch_bounds__(256) void agg_kernel(AggArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x;
+  const int total = a.BH * a.nblk;
+  const int wblk = xcd_swizzle(blockIdx.x, total);
+  const int bh = wblk / a.nblk;
+  const int i0 = (wblk - bh * a.nblk) * a.ti;
+  const int ntok = min(a.ti, a.N - i0);
+  const int dout = a.dout;
+  const bool stage_z = a.merged && a.H > 1;
 
-// standard / depthwise-separable: one block per token
-template <typename T>
-__global__ __launch_bounds__(256) void agg_gen_kernel(AggArgs a) {
-  extern __shared__ float sm[];
-  const int64_t g = blockIdx.x;
-  const int64_t bh = g / a.N;
-  float w[KCAP];
-  int ix[KCAP];
-  weights(a, g, w, ix);
-  const T* V = static_cast<const T*>(a.v) + bh * a.N * a.dkp;
-  const T* W0 = static_cast<const T*>(a.w0);
-  float* P = sm;                         // (K, din)
-  float* t1 = sm + a.K * a.din;          // (din) depthwise stage of dw-separable
-  for (int e = threadIdx.x; e < a.K * a.din; e += 256) {
-    const int r = e / a.din, c = e - r * a.din;
-    float wr = 0.0f;
-    int jr = 0;
-#pragma unroll
-    for (int q = 0; q < KCAP; ++q)
-      if (q == r) { wr = w[q]; jr = ix[q]; }
-    P[e] = wr * ldf(V + (int64_t)jr * a.dkp + c);
-  }
-  __syncthreads();
-  T* y = static_cast<T*>(a.y) + g * a.dout;
-  if (a.conv == CNNA_CONV_STANDARD) {
-    for (int o = threadIdx.x; o < a.dout; o += 256) {
-      float acc = 0.0f;
-      const T* wo = W0 + (int64_t)o * a.din * a.K;
-      for (int c = 0; c < a.din; ++c)
-        for (int r = 0; r < a.K; ++r) acc += ldf(wo + c * a.K + r) * P[r * a.din + c];
-      stf(y + o, acc);
+  // LDS carve-up
+  float* sW = reinterpret_cast<float*>(smem);                       // (K, dout) conv weights
+  float* sw = sW + (COPY ? 0 : a.K * dout);                         // (ti, K) neighbour weights
+  int* sj = reinterpret_cast<int*>(sw + (COPY ? 0 : a.ti * a.K));   // (ti, K) neighbour indices
+  T* stage = reinterpret_cast<T*>(sj + (COPY ? 0 : a.ti * a.K));    // (na, NP)
+  // staged row pitch: a multiple of the vector width, so whole vectors land aligned
+  const int NP = (int)cnna_round_up((size_t)a.N, 8) + 8;
+  const int64_t F0 = (int64_t)i0 * dout;
+  const int a_lo = (int)(F0 / a.N);
+
+  if (!COPY) {
+    const T* W0 = static_cast<const T*>(a.w0);
+    for (int e = tid; e < a.K * dout; e += 256) {
+      const int c = e / a.K, r = e - c * a.K;
+      sW[r * dout + c] = ldf(W0 + e);
     }
-  } else {
-    const T* W1 = static_cast<const T*>(a.w1);
-    for (int c = threadIdx.x; c < a.din; c += 256) {
-      float acc = 0.0f;
-      for (int r = 0; r < a.K; ++r) acc += ldf(W0 + c * a.K + r) * P[r * a.din + c];
-      t1[c] = acc;
+    const int64_t base = ((int64_t)bh * a.N + i0) * a.K;
+    for (int e = tid; e < ntok * a.K; e += 256) {
+      sw[e] = a.w[base + e];
+      sj[e] = a.idx[base + e];
     }
     __syncthreads();
-    for (int o = threadIdx.x; o < a.dout; o += 256) {
-      float acc = 0.0f;
-      for (int c = 0; c < a.din; ++c) acc += ldf(W1 + (int64_t)o * a.din + c) * t1[c];
-      stf(y + o, acc);
+  }
+
+  const int LPT = a.lpt;                 // lanes per token (power of two)
+  const int g = tid & (LPT - 1);
+  const int c0 = g * VW;
+  const T* V = static_cast<const T*>(a.v) + (int64_t)bh * a.N * a.dkp;
+  const int b = bh / a.H, h = bh - b * a.H;
+
+  for (int tt = tid / LPT; tt < ntok; tt += 256 / LPT) {
+    if (c0 >= dout) continue;
+    const int i = i0 + tt;
+    float acc[VW];
+    if (COPY) {
+      Vec<T, VW>::load(static_cast<const T*>(a.v) + ((int64_t)bh * a.N + i) * dout + c0, acc);
+    } else {
+#pragma unroll
+      for (int u = 0; u < VW; ++u) acc[u] = 0.0f;
+      for (int r = 0; r < a.K; ++r) {
+        const int j = sj[tt * a.K + r];
+        const float wr = sw[tt * a.K + r];
+        float vv[VW];
+        Vec<T, VW>::load(V + (int64_t)j * a.dkp + c0, vv);
+#pragma unroll
+        for (int u = 0; u < VW; ++u) acc[u] += sW[r * dout + c0 + u] * (wr * vv[u]);
+      }
     }
+    if (stage_z) {
+      const int64_t f0 = (int64_t)i * dout + c0;
+      int aa = (int)(f0 / a.N);
+      int t = (int)(f0 - (int64_t)aa * a.N);
+      if (VW > 1 && t % VW == 0 && t + VW <= a.N) {
+        Vec<T, VW>::store(stage + (aa - a_lo) * NP + t, acc);   // one 16-byte LDS write
+      } else {
+#pragma unroll
+        for (int u = 0; u < VW; ++u) {
+          stf(stage + (aa - a_lo) * NP + t, acc[u]);
+          if (++t == a.N) { t = 0; ++aa; }
+        }
+      }
+    } else if (a.merged) {
+      // H == 1: Z[b, i, c] = y[b, c, i] (layers.py:248-249, 255-256)
+      Vec<T, VW>::store(static_cast<T*>(a.out) + ((int64_t)b * a.N + i) * a.C + c0, acc);
+    } else {
+      Vec<T, VW>::store(static_cast<T*>(a.out) + ((int64_t)bh * a.N + i) * dout + c0, acc);
+    }
+  }
+  if (!stage_z) return;
+  __syncthreads();
+
+  // write the staged flat range into Z: lanes run along the columns a of a row t
+  const int64_t F1 = (int64_t)(i0 + ntok) * dout;
+  const int na = (int)((F1 - 1) / a.N) - a_lo + 1;
+  const int rows_per_it = 256 / na;
+  const int ar = tid % na, trow = tid / na;
+  if (trow >= rows_per_it) return;
+  T* Z = static_cast<T*>(a.out) + (int64_t)b * a.N * a.C + h * dout + a_lo + ar;
+  const int64_t fa = (int64_t)(a_lo + ar) * a.N;
+  for (int t = trow; t < a.N; t += rows_per_it) {
+    const int64_t f = fa + t;
+    if (f < F0 || f >= F1) continue;
+    Z[(int64_t)t * a.C] = stage[ar * NP + t];
   }
 }
 
-template <typename T>
-int launch_t(const AggArgs& a, hipStream_t s) {
-  const int64_t tokens = (int64_t)a.BH * a.N;
-  if (a.conv == CNNA_CONV_DEPTHWISE) {
-    hipLaunchKernelGGL(agg_dw_kernel<T>, dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0, s, a);
-  } else {
-    const size_t smem = ((size_t)a.K * a.din + a.din) * sizeof(float);
-    hipLaunchKernelGGL(agg_gen_kernel<T>, dim3((unsigned)tokens), dim3(256), smem, s, a);
+template <typename T, bool COPY>
+int launch_vw(const AggArgs& a0, hipStream_t s) {
+  AggArgs a = a0;
+  constexpr int V = 16 / sizeof(T);
+  const bool vec = (a.dout % V == 0) && (COPY || a.dkp % V == 0);
+  const int vw = vec ? V : 1;
+  int lpt = 1;
+  while (lpt < (a.dout + vw - 1) / vw) lpt <<= 1;
+  if (lpt > 256) return CNNA_ERR_SHAPE;
+  a.lpt = lpt;
+  // tokens per block: about eight Z columns per row when merging, within LDS
+  const bool stage_z = a.merged && a.H > 1;
+  int ti = 64;
+  if (stage_z) {
+    ti = (int)cnna_round_up((size_t)((8LL * a.N + a.dout - 1) / a.dout), 16);
+    ti = ti < 16 ? 16 : (ti > 256 ? 256 : ti);
   }
+  auto lds = [&](int t) {
+    size_t n = COPY ? 0 : ((size_t)a.K * a.dout * 4 + (size_t)t * a.K * 8);
+    if (stage_z) {
+      const int na = (int)(((int64_t)t * a.dout - 1) / a.N) + 2;
+      if (na > 256) return (size_t)1 << 40;
+      n += (size_t)na * (cnna_round_up((size_t)a.N, 8) + 8) * sizeof(T);
+    }
+    return n;
+  };
+  while (ti > 1 && lds(ti) > 96 * 1024) ti >>= 1;
+  if (lds(ti) > 96 * 1024) return CNNA_ERR_SHAPE;
+  a.ti = ti;
+  a.nblk = (a.N + ti - 1) / ti;
+  dim3 grid(a.BH * a.nblk);
+  if (vec)
+    hipLaunchKernelGGL((agg_kernel<T, V, COPY>), grid, dim3(256), lds(ti), s, a);
+  else
+    hipLaunchKernelGGL((agg_kernel<T, 1, COPY>), grid, dim3(256), lds(ti), s, a);
   return (int)hipGetLastError();
 }
 
@@ -135,8 +193,14 @@ int launch_t(const AggArgs& a, hipStream_t s) {
 
 int launch_aggregate(int dtype, const AggArgs& a, hipStream_t s) {
   if (a.BH <= 0 || a.N <= 0) return 0;
-  if (a.K > KCAP) return CNNA_ERR_K_RANGE;
-  if (dtype == CNNA_BF16) return launch_t<uint16_t>(a, s);
-  if (dtype == CNNA_F32) return launch_t<float>(a, s);
+  if (dtype == CNNA_BF16) return launch_vw<uint16_t, false>(a, s);
+  if (dtype == CNNA_F32) return launch_vw<float, false>(a, s);
+  return CNNA_ERR_DTYPE;
+}
+
+int launch_merge(int dtype, const AggArgs& a, hipStream_t s) {
+  if (a.BH <= 0 || a.N <= 0) return 0;
+  if (dtype == CNNA_BF16) return launch_vw<uint16_t, true>(a, s);
+  if (dtype == CNNA_F32) return launch_vw<float, true>(a, s);
   return CNNA_ERR_DTYPE;
 }

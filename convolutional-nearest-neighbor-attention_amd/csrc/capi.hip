@@ -137,7 +137,7 @@ int cnna_project_qkv(const cnna_desc* d, const void* x, int64_t ldx, const int32
 }
 
 int cnna_select(const cnna_desc* d, const void* k, const void* q, const float* kn, const float* qn,
-                const int32_t* cand, int32_t* idx, float* vals, void* stream) {
+                const int32_t* cand, int32_t* idx, float* vals, float* w, void* stream) {
   int st = cnna_check_desc(d);
   if (st) return st;
   if (!k || !q || !idx || !vals) return CNNA_ERR_NULL;
@@ -147,7 +147,7 @@ int cnna_select(const cnna_desc* d, const void* k, const void* q, const float* k
   SelArgs a;
   memset(&a, 0, sizeof(a));
   a.k = k; a.q = q; a.kn = kn; a.qn = qn; a.cand = d->sampled ? cand : nullptr;
-  a.idx = idx; a.vals = vals;
+  a.idx = idx; a.vals = vals; a.w = w; a.softmax = d->softmax;
   a.BH = d->B * d->H; a.N = d->N; a.Nq = d->Nq; a.dkp = dkp_of(d);
   a.K = d->K; a.Ksel = ksel_of(d);
   a.rb_per_bh = (d->N + 127) / 128;
@@ -164,26 +164,82 @@ int cnna_select(const cnna_desc* d, const void* k, const void* q, const float* k
   return launch_select(d->dtype, d->metric == CNNA_EUCLIDEAN, d->sampled, a, (hipStream_t)stream);
 }
 
-int cnna_aggregate(const cnna_desc* d, const void* v, const int32_t* idx, const float* vals,
-                   const void* conv_w0, const void* conv_w1, void* y, void* stream) {
-  int st = cnna_check_desc(d);
-  if (st) return st;
-  if (!v || !idx || !vals || !conv_w0 || !y) return CNNA_ERR_NULL;
-  if (d->conv == CNNA_CONV_DWSEP && !conv_w1) return CNNA_ERR_NULL;
-  AggArgs a;
-  memset(&a, 0, sizeof(a));
-  a.v = v; a.idx = idx; a.vals = vals; a.w0 = conv_w0; a.w1 = conv_w1; a.y = y;
-  a.BH = d->B * d->H; a.N = d->N; a.K = d->K;
-  a.din = din_of(d); a.dout = d->C / d->H; a.dkp = dkp_of(d);
-  a.softmax = d->softmax; a.maximum = d->metric != CNNA_EUCLIDEAN; a.conv = d->conv;
-  return launch_aggregate(d->dtype, a, (hipStream_t)stream);
+size_t cnna_aggregate_workspace(const cnna_desc* d) {
+  if (cnna_check_desc(d)) return 0;
+  const size_t es = elem_size(d->dtype), BH = (size_t)d->B * d->H;
+  const size_t dk = d->C / d->H, din = din_of(d);
+  if (d->conv == CNNA_CONV_DEPTHWISE) return 0;
+  size_t n = cnna_round_up(BH * d->N * dk * es, 256);                      // y
+  if (d->conv == CNNA_CONV_STANDARD) n += cnna_round_up(dk * din * d->K * es, 256);   // W0 permuted
+  else n += cnna_round_up(BH * d->N * din * es, 256);                      // depthwise stage
+  return n;
 }
 
-int cnna_output_proj(const cnna_desc* d, const void* y, const void* Wo, void* out, int64_t ldo,
+int cnna_aggregate(const cnna_desc* d, const void* v, const int32_t* idx, const float* w,
+                   const void* conv_w0, const void* conv_w1, void* z, void* ws, size_t ws_bytes,
+                   void* stream) {
+  int st = cnna_check_desc(d);
+  if (st) return st;
+  if (!v || !idx || !w || !conv_w0 || !z) return CNNA_ERR_NULL;
+  if (d->conv == CNNA_CONV_DWSEP && !conv_w1) return CNNA_ERR_NULL;
+  const size_t need = cnna_aggregate_workspace(d);
+  if (need > 0 && (!ws || ws_bytes < need)) return CNNA_ERR_WORKSPACE;
+  if (need > 0 && !aligned16(ws)) return CNNA_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  const int es = elem_size(d->dtype), BH = d->B * d->H, dk = d->C / d->H, din = din_of(d);
+  const int dkp = dkp_of(d);
+  AggArgs a;
+  memset(&a, 0, sizeof(a));
+  a.idx = idx; a.w = w; a.BH = BH; a.N = d->N; a.K = d->K; a.dkp = dkp; a.H = d->H; a.C = d->C;
+  if (d->conv == CNNA_CONV_DEPTHWISE) {
+    // y = depthwise conv over the gathered neighbours, written merged
+    a.v = v; a.w0 = conv_w0; a.out = z; a.dout = dk; a.merged = 1;
+    return launch_aggregate(d->dtype, a, s);
+  }
+  char* p = static_cast<char*>(ws);
+  void* y = p;
+  p += cnna_round_up((size_t)BH * d->N * dk * es, 256);
+  GemmArgs g;
+  memset(&g, 0, sizeof(g));
+  g.M = BH * d->N;
+  g.Nc = dk;
+  g.ncol_each = dk;
+  g.o[0] = y;
+  g.ldo = dk;
+  if (d->conv == CNNA_CONV_STANDARD) {
+    // y = P @ W0p^T with P[m][r*din + c] = w[m, r] * v[idx[m, r], c] gathered in the A loader
+    void* w0p = p;
+    if ((st = launch_permute_w0(d->dtype, conv_w0, w0p, dk, din, d->K, s))) return st;
+    g.Kd = din * d->K;
+    g.a = v;
+    g.g_idx = idx; g.g_w = w; g.g_K = d->K; g.g_N = d->N; g.g_din = din; g.g_dkp = dkp;
+    g.avec = (din % (16 / es) == 0) && (dkp % (16 / es) == 0) && aligned16(v);
+    g.w[0] = w0p;
+    g.bvec = ((g.Kd * es) % 16 == 0);
+    if ((st = launch_gemm(d->dtype, GEMM_A_GATHER, GEMM_O_PLAIN, g, s))) return st;
+  } else {
+    // depthwise stage (din channels) then the pointwise conv as a GEMM
+    void* t1 = p;
+    a.v = v; a.w0 = conv_w0; a.out = t1; a.dout = din; a.merged = 0;
+    if ((st = launch_aggregate(d->dtype, a, s))) return st;
+    g.Kd = din;
+    g.a = t1;
+    g.lda = din;
+    g.avec = ((din * es) % 16 == 0);
+    g.w[0] = conv_w1;
+    g.bvec = ((din * es) % 16 == 0) && aligned16(conv_w1);
+    if ((st = launch_gemm(d->dtype, GEMM_A_ROWS, GEMM_O_PLAIN, g, s))) return st;
+  }
+  // head merge of y into z
+  a.v = y; a.out = z; a.dout = dk; a.merged = 1; a.w0 = nullptr;
+  return launch_merge(d->dtype, a, s);
+}
+
+int cnna_output_proj(const cnna_desc* d, const void* z, const void* Wo, void* out, int64_t ldo,
                      void* stream) {
   int st = cnna_check_desc(d);
   if (st) return st;
-  if (!y || !Wo || !out) return CNNA_ERR_NULL;
+  if (!z || !Wo || !out) return CNNA_ERR_NULL;
   if (ldo < d->C) return CNNA_ERR_SHAPE;
   const int es = elem_size(d->dtype);
   GemmArgs g;
@@ -191,35 +247,28 @@ int cnna_output_proj(const cnna_desc* d, const void* y, const void* Wo, void* ou
   g.M = d->B * d->N;
   g.Nc = d->C;
   g.Kd = d->C;
-  g.a = y;
+  g.a = z;
   g.lda = d->C;
+  g.avec = ((d->C * es) % 16 == 0) && aligned16(z);
   g.w[0] = Wo;
   g.ncol_each = d->C;
+  g.bvec = ((d->C * es) % 16 == 0) && aligned16(Wo);
   g.o[0] = out;
   g.ldo = ldo;
-  g.bvec = ((d->C * es) % 16 == 0) && aligned16(Wo);
-  if (d->H == 1) {
-    // H == 1: merge is a plain transpose back to (B, N, C) (layers.py:248-249, 255-256)
-    g.avec = ((d->C * es) % 16 == 0) && aligned16(y);
-    return launch_gemm(d->dtype, GEMM_A_ROWS, GEMM_O_PLAIN, g, (hipStream_t)stream);
-  }
-  g.mix_N = d->N;
-  g.mix_H = d->H;
-  g.mix_dk = d->C / d->H;
-  return launch_gemm(d->dtype, GEMM_A_MIXED, GEMM_O_PLAIN, g, (hipStream_t)stream);
+  return launch_gemm(d->dtype, GEMM_A_ROWS, GEMM_O_PLAIN, g, (hipStream_t)stream);
 }
 
 size_t cnna_forward_workspace(const cnna_desc* d) {
   if (cnna_check_desc(d)) return 0;
   const size_t es = elem_size(d->dtype), dkp = dkp_of(d), BH = (size_t)d->B * d->H;
-  const size_t dk = d->C / d->H;
   size_t n = 0;
   n += cnna_round_up(BH * d->Nq * dkp * es, 256);         // q
   n += 2 * cnna_round_up(BH * d->N * dkp * es, 256);      // k, v
   n += cnna_round_up(BH * d->Nq * 4, 256);                // qn
   n += cnna_round_up(BH * d->N * 4, 256);                 // kn
-  n += 2 * cnna_round_up(BH * d->N * d->K * 4, 256);      // idx, vals
-  n += cnna_round_up(BH * d->N * dk * es, 256);           // y
+  n += 3 * cnna_round_up(BH * d->N * d->K * 4, 256);      // idx, vals, w
+  n += cnna_round_up((size_t)d->B * d->N * d->C * es, 256);   // z
+  n += cnna_aggregate_workspace(d);
   return n;
 }
 
@@ -233,7 +282,6 @@ int cnna_forward(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* 
   if (ws_bytes < cnna_forward_workspace(d)) return CNNA_ERR_WORKSPACE;
   if (!aligned16(ws)) return CNNA_ERR_SHAPE;
   const size_t es = elem_size(d->dtype), dkp = dkp_of(d), BH = (size_t)d->B * d->H;
-  const size_t dk = d->C / d->H;
   char* p = static_cast<char*>(ws);
   auto take = [&](size_t bytes) { void* r = p; p += cnna_round_up(bytes, 256); return r; };
   void* q = take(BH * d->Nq * dkp * es);
@@ -243,15 +291,18 @@ int cnna_forward(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* 
   float* kn = static_cast<float*>(take(BH * d->N * 4));
   int32_t* idx = static_cast<int32_t*>(take(BH * d->N * d->K * 4));
   float* vals = static_cast<float*>(take(BH * d->N * d->K * 4));
-  void* y = take(BH * d->N * dk * es);
+  float* w = static_cast<float*>(take(BH * d->N * d->K * 4));
+  void* z = take((size_t)d->B * d->N * d->C * es);
+  const size_t agg_ws = cnna_aggregate_workspace(d);
+  void* aws = take(agg_ws);
   const bool euc = d->metric == CNNA_EUCLIDEAN;
   if ((st = cnna_project_qkv(d, x, ldx, cand, Wq, Wk, Wv, q, k, v, euc ? qn : nullptr,
                              euc ? kn : nullptr, stream)))
     return st;
-  if ((st = cnna_select(d, k, q, euc ? kn : nullptr, euc ? qn : nullptr, cand, idx, vals, stream)))
+  if ((st = cnna_select(d, k, q, euc ? kn : nullptr, euc ? qn : nullptr, cand, idx, vals, w, stream)))
     return st;
-  if ((st = cnna_aggregate(d, v, idx, vals, conv_w0, conv_w1, y, stream))) return st;
-  return cnna_output_proj(d, y, Wo, out, ldo, stream);
+  if ((st = cnna_aggregate(d, v, idx, w, conv_w0, conv_w1, z, aws, agg_ws, stream))) return st;
+  return cnna_output_proj(d, z, Wo, out, ldo, stream);
 }
 
 }  // extern "C"

@@ -14,16 +14,21 @@
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint16_t bf16_t;
+// first-class 16-byte vector (HIP's uint4 is a struct and can defeat register promotion)
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 #define CNNA_DEV __device__ __forceinline__
 
 CNNA_DEV float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-CNNA_DEV uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+// round to nearest even (v_cvt_pk_bf16_f32)
+CNNA_DEV uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+// two floats -> packed bf16 pair (lo, hi)
+CNNA_DEV uint32_t f2bf2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 CNNA_DEV float ldf(const float* p) { return *p; }
@@ -89,4 +94,4 @@ CNNA_DEV float linspace_f32(float start, float end, int steps, int i) {
   return (i < halfway) ? start + step * (float)i : end - step * (float)(steps - i - 1);
 }
 
-inline size_t cnna_round_up(size_t a, size_t b) { return (a + b - 1) / b * b; }
+__host__ __device__ inline size_t cnna_round_up(size_t a, size_t b) { return (a + b - 1) / b * b; }

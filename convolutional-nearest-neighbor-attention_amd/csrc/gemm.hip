@@ -1,10 +1,18 @@
-// MFMA GEMM for the projections: Q/K/V (x @ W^T with head split, layers.py:
-// 264-265, 274, 237-245) and the output projection W_o whose A operand is
-// the reference's head merge read in place (layers.py:247-259, 317, 320).
+// MFMA GEMM  out[m][n] = sum_k A[m][k] * W[n][k]  (nn.Linear: x @ W^T).
 //
-// Tile 128 x 128, 256 threads = 4 waves in a 2 x 2 grid, each wave owns a
-// 64 x 64 block = 2 x 2 v_mfma_f32_32x32x{16 bf16 | 2 f32} accumulators.
-// A and W tiles are staged through LDS (rows padded by 16 bytes).
+// Used for the Q/K/V projections with the head split in the epilogue
+// (layers.py:264-265, 274, 237-245), the output projection W_o (layers.py:320),
+// the standard conv as a gather-GEMM over the K neighbours (layers.py:313 with
+// the prime tensor of layers.py:402-405 built on the fly in the A loader) and
+// the pointwise half of the depthwise-separable conv.
+//
+// Tile 128 x 128 x BK, 256 threads = 4 waves in a 2 x 2 grid, each wave owns a
+// 64 x 64 block = 2 x 2 v_mfma_f32_32x32x{16 bf16 | 2 f32} accumulators.  The
+// MFMA computes the transposed tile (W as the A operand), so each lane ends
+// with 4 consecutive output columns of one row and stores them as one vector.
+// The next k-tile is fetched into registers while the current one is
+// multiplied from LDS (rows padded by 16 bytes).  Blocks are ordered so that
+// all column tiles of a row tile run on the same XCD (shared L2).
 #include "common.h"
 #include "kernels.h"
 
@@ -13,22 +21,155 @@ namespace {
 constexpr int BM = 128, BN = 128;
 
 template <typename T> struct GemmCfg;
-template <> struct GemmCfg<uint16_t> { static constexpr int BK = 32, VEC = 8; };
-template <> struct GemmCfg<float> { static constexpr int BK = 16, VEC = 4; };
+template <> struct GemmCfg<uint16_t> { static constexpr int BK = 64, VEC = 8; };
+template <> struct GemmCfg<float> { static constexpr int BK = 32, VEC = 4; };
 
-template <typename T, int AMODE, int OMODE>
+template <typename T, int VEC>
+union Pack {
+  u32x4_t u;
+  T e[VEC];
+};
+
+// w * (16-byte vector of T), rounded back to T
+CNNA_DEV u32x4_t scale_vec(u32x4_t s, float w, uint16_t) {
+  u32x4_t o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    o[i] = f2bf2(w * __uint_as_float(s[i] << 16), w * __uint_as_float(s[i] & 0xffff0000u));
+  return o;
+}
+CNNA_DEV u32x4_t scale_vec(u32x4_t s, float w, float) {
+  u32x4_t o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = __float_as_uint(w * __uint_as_float(s[i]));
+  return o;
+}
+
+// four consecutive outputs -> one 8-byte (bf16) or 16-byte (fp32) store
+CNNA_DEV void store4(uint16_t* p, float a, float b, float c, float d) {
+  uint2 u;
+  u.x = f2bf2(a, b);
+  u.y = f2bf2(c, d);
+  *reinterpret_cast<uint2*>(p) = u;
+}
+CNNA_DEV void store4(float* p, float a, float b, float c, float d) {
+  *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+}
+
+// FAST: 16-byte loads everywhere and Kd % BK == 0 (decided by the launcher)
+template <typename T, int AMODE, int OMODE, bool FAST>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   using M_ = Mfma<T>;
   constexpr int BK = GemmCfg<T>::BK, VEC = GemmCfg<T>::VEC;
-  constexpr int LDS_STRIDE = BK + VEC;  // elements; rows stay 16-byte aligned
-  __shared__ __attribute__((aligned(16))) T As[BM * LDS_STRIDE];
-  __shared__ __attribute__((aligned(16))) T Bs[BN * LDS_STRIDE];
+  constexpr int LDS_STRIDE = BK + VEC;      // elements; rows stay 16-byte aligned
+  constexpr int VPR = BK / VEC;             // 16-byte vectors per tile row
+  constexpr int NV = BM * VPR / 256;        // vectors per thread per operand tile
+  __shared__ __attribute__((aligned(16))) T smem_ab[(BM + BN) * LDS_STRIDE];
+  T* As = smem_ab;
+  T* Bs = smem_ab + BM * LDS_STRIDE;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  const int ncol = (g.Nc + BN - 1) / BN;
+  const int nrow = (g.M + BM - 1) / BM;
+  const int wid = xcd_swizzle(blockIdx.x, ncol * nrow);
+  const int n0 = (wid % ncol) * BN, m0 = (wid / ncol) * BM;
   const T* A = static_cast<const T*>(g.a);
 
+  // per-thread rows of the A and W tiles
+  int rowv[NV], kvv[NV];
+  const T* arow_ptr[NV];
+  const T* wrow_ptr[NV];
+  bool arow_ok[NV], wrow_ok[NV];
+  int64_t gather_base[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = tid + i * 256;
+    rowv[i] = e / VPR;
+    kvv[i] = (e % VPR) * VEC;
+    const int m = m0 + rowv[i];
+    arow_ok[i] = m < g.M;
+    int64_t sr = arow_ok[i] ? m : 0;
+    if (AMODE == GEMM_A_ROWS && g.arow != nullptr && arow_ok[i]) {
+      const int b = m / g.a_rows, rr = m - b * g.a_rows;
+      sr = (int64_t)b * g.a_src_rows + g.arow[rr];
+    }
+    arow_ptr[i] = A + sr * g.lda;
+    const int mc = arow_ok[i] ? m : g.M - 1;
+    gather_base[i] = (AMODE == GEMM_A_GATHER) ? (int64_t)mc - (mc % g.g_N) : 0;
+    const int n = n0 + rowv[i];
+    wrow_ok[i] = n < g.Nc;
+    const int mat = wrow_ok[i] ? n / g.ncol_each : 0;
+    const int rn = wrow_ok[i] ? n - mat * g.ncol_each : 0;
+    wrow_ptr[i] = static_cast<const T*>(g.w[mat]) + (int64_t)rn * g.Kd;
+  }
+
+  Pack<T, VEC> ra[NV], rw[NV];
+  auto fetch = [&](int k0) __attribute__((always_inline)) {
+    if (FAST) {
+      // every vector in range (rows clamped; Kd % BK == 0): no branches, so
+      // the loads stay in flight while the previous tile is multiplied
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int k = k0 + kvv[i];
+        if (AMODE == GEMM_A_ROWS) {
+          ra[i].u = *reinterpret_cast<const u32x4_t*>(arow_ptr[i] + k);
+        } else {
+          const int m = min(m0 + rowv[i], g.M - 1);
+          const int r = k / g.g_din, c = k - r * g.g_din;
+          const int j = g.g_idx[(int64_t)m * g.g_K + r];
+          const float wr = g.g_w[(int64_t)m * g.g_K + r];
+          ra[i].u = scale_vec(*reinterpret_cast<const u32x4_t*>(A + (gather_base[i] + j) * g.g_dkp + c), wr, T(0));
+        }
+        rw[i].u = *reinterpret_cast<const u32x4_t*>(wrow_ptr[i] + k);
+      }
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int k = k0 + kvv[i];
+      // ---- A
+      if (AMODE == GEMM_A_ROWS) {
+        if (arow_ok[i] && g.avec && k + VEC <= g.Kd) {
+          ra[i].u = *reinterpret_cast<const u32x4_t*>(arow_ptr[i] + k);
+        } else {
+#pragma unroll
+          for (int t = 0; t < VEC; ++t)
+            ra[i].e[t] = (arow_ok[i] && k + t < g.Kd) ? arow_ptr[i][k + t] : T(0);
+        }
+      } else {
+        const int m = m0 + rowv[i];
+#pragma unroll
+        for (int t = 0; t < VEC; ++t) {
+          float val = 0.0f;
+          if (arow_ok[i] && k + t < g.Kd) {
+            const int r = (k + t) / g.g_din, c = (k + t) - r * g.g_din;
+            const int j = g.g_idx[(int64_t)m * g.g_K + r];
+            val = g.g_w[(int64_t)m * g.g_K + r] * ldf(A + (gather_base[i] + j) * g.g_dkp + c);
+          }
+          stf(&ra[i].e[t], val);
+        }
+      }
+      // ---- W
+      if (wrow_ok[i] && g.bvec && k + VEC <= g.Kd) {
+        rw[i].u = *reinterpret_cast<const u32x4_t*>(wrow_ptr[i] + k);
+      } else {
+#pragma unroll
+        for (int t = 0; t < VEC; ++t)
+          rw[i].e[t] = (wrow_ok[i] && k + t < g.Kd) ? wrow_ptr[i][k + t] : T(0);
+      }
+    }
+  };
+  auto stash = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      *reinterpret_cast<u32x4_t*>(&As[rowv[i] * LDS_STRIDE + kvv[i]]) = ra[i].u;
+      *reinterpret_cast<u32x4_t*>(&Bs[rowv[i] * LDS_STRIDE + kvv[i]]) = rw[i].u;
+    }
+  };
+
+  // acc[i][j] holds the transposed 32 x 32 block: rows = output columns
+  // n0 + wn*64 + j*32 + .., columns = output rows m0 + wm*64 + i*32 + lane%32
   f32x16_t acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -37,82 +178,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  // per-thread source rows for the A_ROWS / W loads (2 vectors each)
-  constexpr int VPR = BK / VEC;  // vectors per tile row (4)
-  const T* arow_ptr[2];
-  bool arow_ok[2];
-  const T* wrow_ptr[2];
-  bool wrow_ok[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int e = tid + i * 256;
-    const int r = e / VPR;
-    const int m = m0 + r;
-    arow_ok[i] = m < g.M;
-    int64_t sr = m;
-    if (AMODE == GEMM_A_ROWS && g.arow != nullptr && arow_ok[i]) {
-      const int b = m / g.a_rows, rr = m - b * g.a_rows;
-      sr = (int64_t)b * g.a_src_rows + g.arow[rr];
-    }
-    arow_ptr[i] = A + (arow_ok[i] ? sr : 0) * g.lda;
-    const int n = n0 + r;
-    wrow_ok[i] = n < g.Nc;
-    const int mat = wrow_ok[i] ? n / g.ncol_each : 0;
-    const int rn = wrow_ok[i] ? n - mat * g.ncol_each : 0;
-    wrow_ptr[i] = static_cast<const T*>(g.w[mat]) + (int64_t)rn * g.Kd;
-  }
-
+  fetch(0);
   for (int k0 = 0; k0 < g.Kd; k0 += BK) {
-    // ---- stage A
-    if (AMODE == GEMM_A_ROWS) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int e = tid + i * 256;
-        const int r = e / VPR, kv = (e % VPR) * VEC;
-        const int k = k0 + kv;
-        T* dst = &As[r * LDS_STRIDE + kv];
-        if (arow_ok[i] && g.avec && k + VEC <= g.Kd) {
-          *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(arow_ptr[i] + k);
-        } else {
-#pragma unroll
-          for (int t = 0; t < VEC; ++t)
-            dst[t] = (arow_ok[i] && k + t < g.Kd) ? arow_ptr[i][k + t] : T(0);
-        }
-      }
-    } else {
-      // head-merge gather: consecutive threads read consecutive tokens t
-      const T* Y = A;
-      const int64_t head_sz = (int64_t)g.mix_N * g.mix_dk;
-#pragma unroll 4
-      for (int e = tid; e < BM * BK; e += 256) {
-        const int r = e % BM, kc = e / BM;
-        const int m = m0 + r, k = k0 + kc;
-        T val = T(0);
-        if (m < g.M && k < g.Kd) {
-          const int b = m / g.mix_N, t = m - b * g.mix_N;
-          const int h = k / g.mix_dk, c = k - h * g.mix_dk;
-          val = Y[((int64_t)b * g.mix_H + h) * head_sz + (int64_t)c * g.mix_N + t];
-        }
-        As[r * LDS_STRIDE + kc] = val;
-      }
-    }
-    // ---- stage W
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int e = tid + i * 256;
-      const int r = e / VPR, kv = (e % VPR) * VEC;
-      const int k = k0 + kv;
-      T* dst = &Bs[r * LDS_STRIDE + kv];
-      if (wrow_ok[i] && g.bvec && k + VEC <= g.Kd) {
-        *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(wrow_ptr[i] + k);
-      } else {
-#pragma unroll
-        for (int t = 0; t < VEC; ++t)
-          dst[t] = (wrow_ok[i] && k + t < g.Kd) ? wrow_ptr[i][k + t] : T(0);
-      }
-    }
+    stash();
     __syncthreads();
-
+    if (k0 + BK < g.Kd) fetch(k0 + BK);
 #pragma unroll
     for (int ks = 0; ks < BK / M_::KC; ++ks) {
       const int kk = ks * M_::KC + (lane >> 5) * M_::KL;
@@ -125,57 +195,173 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = M_::mma(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < 2; ++j) acc[i][j] = M_::mma(bfr[j], af[i], acc[i][j]);
     }
     __syncthreads();
   }
 
-  // ---- epilogue
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-    if (n >= g.Nc) continue;
-    T* obase;
-    int64_t ocol;
-    if (OMODE == GEMM_O_HEADSPLIT) {
-      const int mat = n / g.ncol_each, nn = n - mat * g.ncol_each;
-      const int h = nn / g.o_dk, c = nn - h * g.o_dk;
-      obase = static_cast<T*>(g.o[mat]);
-      ocol = (int64_t)h * g.o_rows * g.o_dkp + c;
-    } else {
-      obase = static_cast<T*>(g.o[0]);
-      ocol = n;
-    }
+  if (sizeof(T) == 2 && g.ostage) {
+    // ---- bf16 epilogue through LDS: the 128 x 128 tile is staged (reusing the
+    // operand buffers) and written back as whole 16-byte row segments
+    constexpr int CP = BN + 8;                              // staged row pitch
+    T* Cs = As;                                             // 128 * 136 <= As + Bs
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = m0 + wm * 64 + i * 32 + mfma_row(v, lane);
-        if (m >= g.M) continue;
-        int64_t off;
-        if (OMODE == GEMM_O_HEADSPLIT) {
-          const int b = m / g.o_rows, r = m - b * g.o_rows;
-          off = ((int64_t)b * g.o_H * g.o_rows + r) * g.o_dkp + ocol;
-        } else {
-          off = (int64_t)m * g.ldo + ocol;
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq) {
+          const int ml = wm * 64 + i * 32 + (lane & 31);
+          const int nl = wn * 64 + j * 32 + vq * 8 + (lane >> 5) * 4;
+          const f32x16_t& a = acc[i][j];
+          uint2 u;
+          u.x = f2bf2(a[vq * 4], a[vq * 4 + 1]);
+          u.y = f2bf2(a[vq * 4 + 2], a[vq * 4 + 3]);
+          *reinterpret_cast<uint2*>(&Cs[ml * CP + nl]) = u;
         }
-        stf(obase + off, acc[i][j][v]);
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < (BM * BN / 8) / 256; ++it) {
+      const int e = tid + it * 256;
+      const int ml = e >> 4, nl = (e & 15) * 8;
+      const int m = m0 + ml, n = n0 + nl;
+      if (m >= g.M || n >= g.Nc) continue;
+      const u32x4_t val = *reinterpret_cast<const u32x4_t*>(&Cs[ml * CP + nl]);
+      T* dst;
+      bool whole = n + 8 <= g.Nc;
+      if (OMODE == GEMM_O_HEADSPLIT) {
+        const int mat = n / g.ncol_each, nn = n - mat * g.ncol_each;
+        const int h = nn / g.o_dk, c = nn - h * g.o_dk;
+        const int b = m / g.o_rows, r = m - b * g.o_rows;
+        dst = static_cast<T*>(g.o[mat]) + (((int64_t)b * g.o_H + h) * g.o_rows + r) * g.o_dkp + c;
+        whole = whole && (c + 8 <= g.o_dk);
+      } else {
+        dst = static_cast<T*>(g.o[0]) + (int64_t)m * g.ldo + n;
       }
+      if (whole) {
+        *reinterpret_cast<u32x4_t*>(dst) = val;
+      } else {
+        for (int u = 0; u < 8 && n + u < g.Nc; ++u) {
+          const T v = Cs[ml * CP + nl + u];
+          if (OMODE == GEMM_O_HEADSPLIT) {
+            const int nu = n + u;
+            const int mat = nu / g.ncol_each, nn = nu - mat * g.ncol_each;
+            const int h = nn / g.o_dk, c = nn - h * g.o_dk;
+            const int b = m / g.o_rows, r = m - b * g.o_rows;
+            static_cast<T*>(g.o[mat])[(((int64_t)b * g.o_H + h) * g.o_rows + r) * g.o_dkp + c] = v;
+          } else {
+            dst[u] = v;
+          }
+        }
+      }
+    }
+    return;
   }
+
+  // ---- epilogue: lane owns row m (per i) and columns nq..nq+3 (per j, vq)
+  int64_t roff[2];
+  bool mok[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int m = m0 + wm * 64 + i * 32 + (lane & 31);
+    mok[i] = m < g.M;
+    const int mc = mok[i] ? m : 0;
+    if (OMODE == GEMM_O_HEADSPLIT) {
+      const int b = mc / g.o_rows, r = mc - b * g.o_rows;
+      roff[i] = ((int64_t)b * g.o_H * g.o_rows + r) * g.o_dkp;
+    } else {
+      roff[i] = (int64_t)mc * g.ldo;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int vq = 0; vq < 4; ++vq) {
+      const int nq = n0 + wn * 64 + j * 32 + vq * 8 + (lane >> 5) * 4;
+      if (nq >= g.Nc) continue;
+      T* ob;
+      int64_t oc;
+      bool vec = g.ovec && nq + 3 < g.Nc;
+      if (OMODE == GEMM_O_HEADSPLIT) {
+        const int mat = nq / g.ncol_each, nn = nq - mat * g.ncol_each;
+        const int h = nn / g.o_dk, c = nn - h * g.o_dk;
+        ob = static_cast<T*>(g.o[mat]);
+        oc = (int64_t)h * g.o_rows * g.o_dkp + c;
+        vec = vec && (c + 3 < g.o_dk);
+      } else {
+        ob = static_cast<T*>(g.o[0]);
+        oc = nq;
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        if (!mok[i]) continue;
+        const f32x16_t& a = acc[i][j];
+        if (vec) {
+          store4(ob + roff[i] + oc, a[vq * 4], a[vq * 4 + 1], a[vq * 4 + 2], a[vq * 4 + 3]);
+        } else {
+          // tile edge: element by element (the head split re-derived per column)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int n = nq + u;
+            if (n >= g.Nc) break;
+            if (OMODE == GEMM_O_HEADSPLIT) {
+              const int mat = n / g.ncol_each, nn = n - mat * g.ncol_each;
+              const int h = nn / g.o_dk, c = nn - h * g.o_dk;
+              stf(static_cast<T*>(g.o[mat]) + roff[i] + (int64_t)h * g.o_rows * g.o_dkp + c, a[vq * 4 + u]);
+            } else {
+              stf(ob + roff[i] + n, a[vq * 4 + u]);
+            }
+          }
+        }
+      }
+    }
 }
 
-template <typename T>
-int launch_t(int amode, int omode, const GemmArgs& g, hipStream_t s) {
-  dim3 grid((g.Nc + BN - 1) / BN, (g.M + BM - 1) / BM);
+template <typename T, bool FAST>
+int launch_f(int amode, int omode, const GemmArgs& g, hipStream_t s) {
+  dim3 grid(((g.Nc + BN - 1) / BN) * ((g.M + BM - 1) / BM));
   if (amode == GEMM_A_ROWS && omode == GEMM_O_HEADSPLIT)
-    hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_HEADSPLIT>), grid, dim3(256), 0, s, g);
+    hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_HEADSPLIT, FAST>), grid, dim3(256), 0, s, g);
   else if (amode == GEMM_A_ROWS && omode == GEMM_O_PLAIN)
-    hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN>), grid, dim3(256), 0, s, g);
-  else if (amode == GEMM_A_MIXED && omode == GEMM_O_PLAIN)
-    hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_MIXED, GEMM_O_PLAIN>), grid, dim3(256), 0, s, g);
+    hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN, FAST>), grid, dim3(256), 0, s, g);
+  else if (amode == GEMM_A_GATHER && omode == GEMM_O_PLAIN)
+    hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_GATHER, GEMM_O_PLAIN, FAST>), grid, dim3(256), 0, s, g);
   else
     return CNNA_ERR_OPTION;
   return (int)hipGetLastError();
+}
+
+template <typename T>
+int launch_t(int amode, int omode, const GemmArgs& g0, hipStream_t s) {
+  GemmArgs g = g0;
+  // vector epilogue: 4 consecutive columns land contiguously and aligned
+  const int es = sizeof(T);
+  bool ovec = true;
+  for (int i = 0; i < 3; ++i)
+    if (g.o[i] && ((uintptr_t)g.o[i] % (4 * es)) != 0) ovec = false;
+  if (omode == GEMM_O_PLAIN) ovec = ovec && (g.ldo % 4 == 0);
+  else ovec = ovec && (g.o_dkp % 4 == 0) && (g.ncol_each % 4 == 0) && (g.o_dk % 4 == 0);
+  g.ovec = ovec;
+  // staged bf16 epilogue: 8-column (16-byte) segments stay aligned and inside a head
+  bool ostage = sizeof(T) == 2;
+  for (int i = 0; i < 3; ++i)
+    if (g.o[i] && ((uintptr_t)g.o[i] % 16) != 0) ostage = false;
+  if (omode == GEMM_O_PLAIN) ostage = ostage && (g.ldo % 8 == 0);
+  else ostage = ostage && (g.o_dkp % 8 == 0) && (g.ncol_each % 8 == 0) && (g.o_dk % 8 == 0);
+  g.ostage = ostage;
+  const bool fast = g.avec && g.bvec && (g.Kd % GemmCfg<T>::BK == 0);
+  return fast ? launch_f<T, true>(amode, omode, g, s) : launch_f<T, false>(amode, omode, g, s);
+}
+
+template <typename T>
+__global__ void permute_w0_kernel(const T* w0, T* w0p, int dout, int din, int K) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = (int64_t)dout * din * K;
+  if (e >= total) return;
+  const int o = (int)(e / ((int64_t)din * K));
+  const int rem = (int)(e - (int64_t)o * din * K);
+  const int c = rem / K, r = rem - c * K;
+  w0p[(int64_t)o * din * K + (int64_t)r * din + c] = w0[e];
 }
 
 }  // namespace
@@ -185,4 +371,18 @@ int launch_gemm(int dtype, int amode, int omode, const GemmArgs& g, hipStream_t 
   if (dtype == CNNA_BF16) return launch_t<uint16_t>(amode, omode, g, s);
   if (dtype == CNNA_F32) return launch_t<float>(amode, omode, g, s);
   return CNNA_ERR_DTYPE;
+}
+
+int launch_permute_w0(int dtype, const void* w0, void* w0p, int dout, int din, int K, hipStream_t s) {
+  const int64_t total = (int64_t)dout * din * K;
+  dim3 grid((unsigned)((total + 255) / 256));
+  if (dtype == CNNA_BF16)
+    hipLaunchKernelGGL(permute_w0_kernel<uint16_t>, grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(w0), static_cast<uint16_t*>(w0p), dout, din, K);
+  else if (dtype == CNNA_F32)
+    hipLaunchKernelGGL(permute_w0_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(w0),
+                       static_cast<float*>(w0p), dout, din, K);
+  else
+    return CNNA_ERR_DTYPE;
+  return (int)hipGetLastError();
 }

@@ -1,21 +1,25 @@
-// Implementation of the fused similarity + top-k kernel; included by
+// Implementation of the fused similarity + streaming top-k kernel; included by
 // select_bf16.hip and select_f32.hip so the two dtypes compile in parallel.
-#pragma once
-// Fused similarity + streaming top-k (replaces layers.py:323-340 followed by
-// torch.topk in layers.py:344, 363, 391, 410 and the sampled self mask
-// layers.py:291-292, 304-305).  The N x Nq similarity never reaches HBM.
+//
+// Replaces layers.py:323-340 followed by torch.topk in layers.py:344, 363,
+// 391, 410 and the sampled self mask layers.py:291-292, 304-305.  The N x Nq
+// similarity never reaches HBM.
 //
 // Block = 4 waves; a wave owns 32 tokens of one (batch, head).  Candidate
 // (query) tiles of 64 rows are staged through LDS, double buffered, and each
-// wave computes S^T for its tokens with v_mfma_f32_32x32x{16 bf16|2 f32}:
-// the A operand is the candidate tile and the B operand the wave's 32 key
-// rows (kept in registers), so lane l holds 16 candidates of token l % 32 per
+// wave computes S^T for its tokens with v_mfma_f32_32x32x{16 bf16|2 f32}: the
+// A operand is the candidate tile and the B operand the wave's 32 key rows
+// (kept in registers), so lane l holds 16 candidates of token l % 32 per
 // 32-candidate block; lanes l and l + 32 split a token's candidates.
 //
-// Ranking key (larger is better): dot metrics use acc * kscale (matmul scale
-// 1/sqrt(d_k), cosine inputs are pre-normalised); euclidean uses -d^2 with
-// d^2 = (|k|^2 + |q|^2) - 2 acc, and a negative d^2 (NaN distance in the
-// reference) ranks last.  Ties break by the lowest candidate index.
+// Ranking key (larger is better):
+//   matmul / cosine, sampling 'all': the raw accumulator k.q (the positive
+//     scale 1/sqrt(d_k) is applied to the selected values only);
+//   sampled paths: acc * kscale, with the self-masked candidate set to the
+//     reference's constant;
+//   euclidean: -d^2, d^2 = (|k|^2 + |q|^2) - 2 acc; a negative d^2 (NaN
+//     distance in the reference) ranks last.
+// Ties break by the lowest candidate index.
 //
 // Two passes over the candidates:
 //  1. per lane, the maximum of each 16-candidate group goes into a sorted
@@ -26,21 +30,27 @@
 //     LDS queue (about K + few entries per token).  Queues are merged into a
 //     sorted (key, index) register list when they fill and at the end; after a
 //     merge tau rises to just above the list's K-th key.  The two half-lane
-//     lists are finally merged and written out.
+//     lists are finally merged and written out with the neighbour weights.
+#pragma once
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
 namespace {
 
 constexpr int TJ = 64;      // candidates per tile (two MFMA blocks)
-constexpr int QC = 32;      // queue capacity per lane
+constexpr int QC = 16;      // queue capacity per lane (drained when a lane passes QC - 8)
 constexpr int NT = 256;     // threads per block
 
 template <typename T> struct SelCfg;
 template <> struct SelCfg<uint16_t> { static constexpr int MAXCH = 16, VEC = 8; };  // d <= 256
 template <> struct SelCfg<float> { static constexpr int MAXCH = 64, VEC = 4; };     // d <= 128
 
-CNNA_DEV bool better(float v, int j, float ov, int oj) { return v > ov || (v == ov && j < oj); }
+// (v, j) ranks before (ov, oj): larger key, then lower index (branch-free)
+CNNA_DEV bool better(float v, int j, float ov, int oj) {
+  return (v > ov) | ((v == ov) & (j < oj));
+}
 
 template <int KMAX>
 CNNA_DEV void list_insert(float (&SV)[KMAX], int (&SI)[KMAX], float v, int j) {
@@ -80,11 +90,21 @@ CNNA_DEV float pick(const float (&L)[KMAX], int r) {
   return __int_as_float(t);
 }
 
-// NCH: compile-time upper bound of the MFMA reduction chunks (d / KC)
-template <typename T, int NCH, int KMAX, bool EUC, bool SMP>
-__global__ __launch_bounds__(NT) void select_kernel(SelArgs a) {
+// NCH: number of MFMA reduction chunks (d / KC); EXACT: the head width equals
+// NCH * KC (no per-chunk guards), otherwise NCH is an upper bound.
+// Two blocks (8 waves) per CU where the register footprint allows it without spills.
+// KFR: registers per lane holding the key rows (NCH fragments).
+template <int KFR, int KMAX, bool EUC, bool SMP>
+constexpr int sel_min_blocks() {
+  return (KMAX <= 16 && KFR <= 32 && ((!EUC && !SMP) || KFR * KMAX <= 288)) ? 2 : 1;
+}
+
+template <typename T, int NCH, bool EXACT, int KMAX, bool EUC, bool SMP>
+__global__ __launch_bounds__(NT, (sel_min_blocks<NCH * (sizeof(T) == 2 ? 4 : 1), KMAX, EUC, SMP>()))
+void select_kernel(SelArgs a) {
   using M_ = Mfma<T>;
   constexpr int VEC = SelCfg<T>::VEC;
+  constexpr bool RAW = !EUC && !SMP;     // keys are raw accumulators
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -96,13 +116,14 @@ __global__ __launch_bounds__(NT) void select_kernel(SelArgs a) {
   const bool tvalid = ti < a.N;
   const int tic = tvalid ? ti : a.N - 1;
 
-  const int dkp = a.dkp, nch = dkp / M_::KC;
+  const int dkp = EXACT ? NCH * M_::KC : a.dkp;
+  const int nch = dkp / M_::KC;
   const int QS = dkp + VEC;  // LDS row stride of a candidate tile (elements)
   T* qt = reinterpret_cast<T*>(smem);
   float* qnt = reinterpret_cast<float*>(smem + 2 * TJ * QS * sizeof(T));
   int* cdt = reinterpret_cast<int*>(qnt + 2 * TJ);
   float* qkey = reinterpret_cast<float*>(cdt + 2 * TJ);
-  int* qidx = reinterpret_cast<int*>(qkey + QC * NT);
+  uint16_t* qidx = reinterpret_cast<uint16_t*>(qkey + QC * NT);
 
   const T* Kb = static_cast<const T*>(a.k) + ((int64_t)bh * a.N + tic) * dkp;
   const T* Qb = static_cast<const T*>(a.q) + (int64_t)bh * a.Nq * dkp;
@@ -111,13 +132,18 @@ __global__ __launch_bounds__(NT) void select_kernel(SelArgs a) {
   typename M_::frag kf[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
-    kf[c] = (c < nch) ? M_::load(Kb + c * M_::KC + half * M_::KL) : M_::zero();
+    kf[c] = (EXACT || c < nch) ? M_::load(Kb + c * M_::KC + half * M_::KL) : M_::zero();
+  // wait for the key rows here, so the tile loop carries no vector-memory waits
+  // ahead of its MFMAs (s_waitcnt vmcnt(0))
+  __builtin_amdgcn_s_waitcnt(0x0F70);
 
   const int ntiles = (a.Nq + TJ - 1) / TJ;
   const int vpr = dkp / VEC;  // 16-byte vectors per candidate row
   constexpr int NPF = (TJ * (NCH * Mfma<T>::KC / VEC) + NT - 1) / NT;
 
-  uint4 pf[NPF];
+  // ---- tile staging: unconditional loads of clamped rows (rows >= Nq are
+  // masked when keys are formed), so no load sits behind a branch
+  u32x4_t pf[NPF];
   float pfn = 0.0f;
   int pfc = 0;
   auto fetch = [&](int tile) __attribute__((always_inline)) {
@@ -125,15 +151,15 @@ __global__ __launch_bounds__(NT) void select_kernel(SelArgs a) {
 #pragma unroll
     for (int i = 0; i < NPF; ++i) {
       const int e = tid + i * NT;
-      const int r = e / vpr, cv = e - r * vpr;
-      pf[i] = make_uint4(0, 0, 0, 0);
-      if (r < TJ && j0 + r < a.Nq)
-        pf[i] = *reinterpret_cast<const uint4*>(Qb + (int64_t)(j0 + r) * dkp + cv * VEC);
+      int r = e / vpr;
+      const int cv = e - r * vpr;
+      r = min(j0 + min(r, TJ - 1), a.Nq - 1);
+      pf[i] = *reinterpret_cast<const u32x4_t*>(Qb + (int64_t)r * dkp + cv * VEC);
     }
-    if (tid < TJ) {
-      const int j = j0 + tid;
-      if (EUC) pfn = (j < a.Nq) ? a.qn[(int64_t)bh * a.Nq + j] : 0.0f;
-      if (SMP) pfc = (j < a.Nq) ? a.cand[j] : -1;
+    if (EUC || SMP) {
+      const int j = min(j0 + (tid & (TJ - 1)), a.Nq - 1);
+      if (EUC) pfn = a.qn[(int64_t)bh * a.Nq + j];
+      if (SMP) pfc = a.cand[j];
     }
   };
   auto stash = [&](int buf) __attribute__((always_inline)) {
@@ -142,7 +168,7 @@ __global__ __launch_bounds__(NT) void select_kernel(SelArgs a) {
     for (int i = 0; i < NPF; ++i) {
       const int e = tid + i * NT;
       const int r = e / vpr, cv = e - r * vpr;
-      if (r < TJ) *reinterpret_cast<uint4*>(dst + r * QS + cv * VEC) = pf[i];
+      if (EXACT || r < TJ) *reinterpret_cast<u32x4_t*>(dst + r * QS + cv * VEC) = pf[i];
     }
     if (tid < TJ) {
       if (EUC) qnt[buf * TJ + tid] = pfn;
@@ -152,23 +178,24 @@ __global__ __launch_bounds__(NT) void select_kernel(SelArgs a) {
 
   // S^T tile for this wave: acc[blk][v] = k_ti . q_{j0 + blk*32 + mfma_row(v)}
   auto compute = [&](int buf, f32x16_t (&acc)[2]) __attribute__((always_inline)) {
-    const T* base = qt + buf * TJ * QS;
+    const T* base = qt + buf * TJ * QS + col * QS + half * M_::KL;
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      if (c < nch) {
-        const typename M_::frag a0 = M_::load(base + col * QS + c * M_::KC + half * M_::KL);
-        const typename M_::frag a1 = M_::load(base + (32 + col) * QS + c * M_::KC + half * M_::KL);
+      if (EXACT || c < nch) {
+        const typename M_::frag a0 = M_::load(base + c * M_::KC);
+        const typename M_::frag a1 = M_::load(base + 32 * QS + c * M_::KC);
         acc[0] = M_::mma(a0, kf[c], acc[0]);
         acc[1] = M_::mma(a1, kf[c], acc[1]);
       }
     }
   };
-  // ranking key of one accumulator entry (NaN = not a candidate)
-  auto keyof = [&](float accv, int buf, int jl, int j) __attribute__((always_inline)) -> float {
+  // ranking key of one accumulator entry
+  auto keyof = [&](float accv, int buf, int jl) __attribute__((always_inline)) -> float {
+    if (RAW) return accv;
     float key;
     if (EUC) {
       const float d2 = __builtin_fmaf(-2.0f, accv, kni + qnt[buf * TJ + jl]);
@@ -177,46 +204,81 @@ __global__ __launch_bounds__(NT) void select_kernel(SelArgs a) {
       key = accv * a.kscale;
     }
     if (SMP && cdt[buf * TJ + jl] == ti) key = a.mask_key;
-    return (j < a.Nq) ? key : __builtin_nanf("");
+    return key;
   };
 
-  // drive the double-buffered tile loop; body(buf, j0) per tile
-  auto sweep = [&](auto&& body) __attribute__((always_inline)) {
+  // Software-pipelined tile loop: the MFMAs of tile t+1 are issued before the
+  // VALU work on tile t, so the matrix and vector pipes overlap within a wave.
+  // Tile t lives in LDS buffer t&1; tile t+2 is staged into that buffer once
+  // every wave is done with tile t, and tile t+3 is fetched into registers.
+  // process(acc, buf, j0) consumes one tile's accumulators.
+  auto sweep = [&](auto&& process) __attribute__((always_inline)) {
+    f32x16_t accA[2], accB[2];
     fetch(0);
     stash(0);
+    if (ntiles > 1) {
+      fetch(1);
+      stash(1);
+    }
     __syncthreads();
-    for (int t = 0; t < ntiles; ++t) {
-      const int buf = t & 1;
-      if (t + 1 < ntiles) fetch(t + 1);
-      body(buf, t * TJ);
-      if (t + 1 < ntiles) stash(buf ^ 1);
+    if (ntiles > 2) fetch(2);
+    compute(0, accA);
+    auto step = [&](f32x16_t (&cur)[2], f32x16_t (&nxt)[2], int t) __attribute__((always_inline)) {
+      if (t + 1 < ntiles) compute((t + 1) & 1, nxt);
+      process(cur, t & 1, t * TJ);
+      if (!RAW) __syncthreads();       // process() read this tile's LDS side data
+      if (t + 2 < ntiles) {
+        stash(t & 1);
+        if (t + 3 < ntiles) fetch(t + 3);
+      }
       __syncthreads();
+    };
+    for (int t = 0; t < ntiles; t += 2) {
+      step(accA, accB, t);
+      if (t + 1 < ntiles) step(accB, accA, t + 1);
     }
   };
 
-  float SV[KMAX];
-  int SI[KMAX];
+  // Each lane's sorted (key, index) list lives in LDS (column tid of lk/li):
+  // only the drains and the final merge touch it, so it is not held in
+  // registers across the tile loop.  Index 0xffff marks an empty slot.
+  float* lk = reinterpret_cast<float*>(qidx + QC * NT);
+  uint16_t* li = reinterpret_cast<uint16_t*>(lk + KMAX * NT);
 #pragma unroll
-  for (int r = 0; r < KMAX; ++r) { SV[r] = -INFINITY; SI[r] = 0x7fffffff; }
+  for (int r = 0; r < KMAX; ++r) {
+    lk[r * NT + tid] = -INFINITY;
+    li[r * NT + tid] = 0xffff;
+  }
 
   if (a.Ksel > 0) {
     // ---------------- pass 1: group-max bound
     float L[KMAX];
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) L[r] = -INFINITY;
-    sweep([&](int buf, int j0) __attribute__((always_inline)) {
-      f32x16_t acc[2];
-      compute(buf, acc);
+    // MASKED: the tile runs past Nq (only the last one); its extra rows drop out
+    auto bound_tile = [&](const f32x16_t (&acc)[2], int buf, int j0, auto MASKED)
+                          __attribute__((always_inline)) {
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
-        float gm = -INFINITY;
+        float key[16];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int jl = b * 32 + mfma_row(v, lane);
-          gm = fmaxf(gm, keyof(acc[b][v], buf, jl, j0 + jl));
+          key[v] = keyof(acc[b][v], buf, jl);
+          if (decltype(MASKED)::value && j0 + jl >= a.Nq) key[v] = -INFINITY;
         }
+        float gm = key[0];
+#pragma unroll
+        for (int v = 1; v < 15; v += 2) gm = __builtin_fmaxf(gm, __builtin_fmaxf(key[v], key[v + 1]));
+        gm = __builtin_fmaxf(gm, key[15]);
         bound_insert<KMAX>(L, gm);
       }
+    };
+    sweep([&](const f32x16_t (&acc)[2], int buf, int j0) __attribute__((always_inline)) {
+      if (j0 + TJ <= a.Nq)
+        bound_tile(acc, buf, j0, std::false_type{});
+      else
+        bound_tile(acc, buf, j0, std::true_type{});
     });
     {
       float P[KMAX];
@@ -230,42 +292,60 @@ __global__ __launch_bounds__(NT) void select_kernel(SelArgs a) {
     // ---------------- pass 2: filter + queue
     int cnt = 0;
     float* myk = qkey + tid;
-    int* myi = qidx + tid;
+    uint16_t* myi = qidx + tid;
     auto drain = [&]() __attribute__((always_inline)) {
+      float SV[KMAX];
+      int SI[KMAX];
+#pragma unroll
+      for (int r = 0; r < KMAX; ++r) {
+        SV[r] = lk[r * NT + tid];
+        const int j = li[r * NT + tid];
+        SI[r] = (j == 0xffff) ? 0x7fffffff : j;
+      }
       for (int e = 0; __any(e < cnt); ++e) {
-        if (e < cnt) list_insert<KMAX>(SV, SI, myk[e * NT], myi[e * NT]);
+        // lanes past their count insert a sentinel, which never moves the list
+        const bool live = e < cnt;
+        const float v = live ? myk[e * NT] : -INFINITY;
+        const int j = live ? (int)myi[e * NT] : 0x7fffffff;
+        list_insert<KMAX>(SV, SI, v, j);
+      }
+#pragma unroll
+      for (int r = 0; r < KMAX; ++r) {
+        lk[r * NT + tid] = SV[r];
+        li[r * NT + tid] = (uint16_t)(SI[r] == 0x7fffffff ? 0xffff : SI[r]);
       }
       cnt = 0;
       const int kth = pick<KMAX>(SI, a.Ksel - 1);
       if (kth != 0x7fffffff) tau = fmaxf(tau, next_up(pick<KMAX>(SV, a.Ksel - 1)));
     };
-    sweep([&](int buf, int j0) __attribute__((always_inline)) {
-      f32x16_t acc[2];
-      compute(buf, acc);
+    auto filter_tile = [&](const f32x16_t (&acc)[2], int buf, int j0, auto MASKED)
+                           __attribute__((always_inline)) {
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
-        if (__any(cnt > QC - 16)) drain();
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
+          if (v % 8 == 0 && __any(cnt > QC - 8)) drain();
           const int jl = b * 32 + mfma_row(v, lane);
-          const float key = keyof(acc[b][v], buf, jl, j0 + jl);
-          if (key >= tau) {
-            myk[cnt * NT] = key;
-            myi[cnt * NT] = j0 + jl;
-            ++cnt;
-          }
+          float key = keyof(acc[b][v], buf, jl);
+          if (decltype(MASKED)::value && j0 + jl >= a.Nq) key = __builtin_nanf("");
+          // branch-free append: write at the current slot, keep it only if it passed
+          // (cnt <= QC - 1 here: the block starts with cnt <= QC - 16)
+          myk[cnt * NT] = key;
+          myi[cnt * NT] = (uint16_t)(j0 + jl);
+          cnt += (key >= tau) ? 1 : 0;
         }
       }
+    };
+    sweep([&](const f32x16_t (&acc)[2], int buf, int j0) __attribute__((always_inline)) {
+      if (j0 + TJ <= a.Nq)
+        filter_tile(acc, buf, j0, std::false_type{});
+      else
+        filter_tile(acc, buf, j0, std::true_type{});
     });
     drain();
   }
 
   // ---------------- merge the two half-lane lists and write out
-#pragma unroll
-  for (int r = 0; r < KMAX; ++r) {
-    qkey[r * NT + tid] = SV[r];
-    qidx[r * NT + tid] = SI[r];
-  }
   __syncthreads();
   if (half == 0 && tvalid) {
     const int64_t o = ((int64_t)bh * a.N + ti) * a.K;
@@ -278,14 +358,15 @@ __global__ __launch_bounds__(NT) void select_kernel(SelArgs a) {
     int ia = 0, ib = 0;
     for (int r = 0; r < a.Ksel; ++r) {
       const int ra = ia < KMAX ? ia : KMAX - 1, rb2 = ib < KMAX ? ib : KMAX - 1;
-      const float va = qkey[ra * NT + tid], vb = qkey[rb2 * NT + tid + 32];
-      const int ja = qidx[ra * NT + tid], jb = qidx[rb2 * NT + tid + 32];
+      const float va = lk[ra * NT + tid], vb = lk[rb2 * NT + tid + 32];
+      const int ja0 = li[ra * NT + tid], jb0 = li[rb2 * NT + tid + 32];
+      const int ja = ja0 == 0xffff ? 0x7fffffff : ja0, jb = jb0 == 0xffff ? 0x7fffffff : jb0;
       const bool ta = (ia < KMAX) && (ib >= KMAX || better(va, ja, vb, jb));
       const float key = ta ? va : vb;
       const int j = ta ? ja : jb;
       ia += ta ? 1 : 0;
       ib += ta ? 0 : 1;
-      float val = key;
+      float val = RAW ? key * a.kscale : key;
       int tok = j;
       if (SMP) tok = a.cand[j];
       if (EUC) val = (key == -INFINITY) ? __builtin_nanf("") : sqrtf(-key);
@@ -293,27 +374,50 @@ __global__ __launch_bounds__(NT) void select_kernel(SelArgs a) {
       a.idx[o + off + r] = tok;
       a.vals[o + off + r] = val;
     }
+    // neighbour weights (layers.py:352-355, 382-385, 394-397, 426-429)
+    if (a.w != nullptr) {
+      if (a.softmax) {
+        float mx = -INFINITY;
+        for (int r = 0; r < a.K; ++r) {
+          const float v = a.vals[o + r];
+          mx = fmaxf(mx, EUC ? -v : v);
+        }
+        float sum = 0.0f;
+        for (int r = 0; r < a.K; ++r) {
+          const float v = a.vals[o + r];
+          const float e = expf((EUC ? -v : v) - mx);
+          a.w[o + r] = e;
+          sum += e;
+        }
+        for (int r = 0; r < a.K; ++r) a.w[o + r] = a.w[o + r] / sum;
+      } else {
+        for (int r = 0; r < a.K; ++r) {
+          const float v = a.vals[o + r];
+          a.w[o + r] = EUC ? 1.0f / (v + 1e-8f) : v;
+        }
+      }
+    }
   }
 }
 
-template <typename T, int NCH, int KMAX>
+template <typename T, int NCH, bool EXACT, int KMAX>
 int launch_k(int euclid, int sampled, const SelArgs& a, size_t smem, dim3 grid, hipStream_t s) {
   if (!euclid && !sampled)
-    hipLaunchKernelGGL((select_kernel<T, NCH, KMAX, false, false>), grid, dim3(NT), smem, s, a);
+    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, false, false>), grid, dim3(NT), smem, s, a);
   else if (!euclid && sampled)
-    hipLaunchKernelGGL((select_kernel<T, NCH, KMAX, false, true>), grid, dim3(NT), smem, s, a);
+    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, false, true>), grid, dim3(NT), smem, s, a);
   else if (euclid && !sampled)
-    hipLaunchKernelGGL((select_kernel<T, NCH, KMAX, true, false>), grid, dim3(NT), smem, s, a);
+    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, true, false>), grid, dim3(NT), smem, s, a);
   else
-    hipLaunchKernelGGL((select_kernel<T, NCH, KMAX, true, true>), grid, dim3(NT), smem, s, a);
+    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, true, true>), grid, dim3(NT), smem, s, a);
   return (int)hipGetLastError();
 }
 
 template <typename T, int NCH>
 int launch_n(int euclid, int sampled, const SelArgs& a, size_t smem, dim3 grid, hipStream_t s) {
-  if (a.Ksel <= 9) return launch_k<T, NCH, 9>(euclid, sampled, a, smem, grid, s);
-  if (a.Ksel <= 16) return launch_k<T, NCH, 16>(euclid, sampled, a, smem, grid, s);
-  if (a.Ksel <= 32) return launch_k<T, NCH, 32>(euclid, sampled, a, smem, grid, s);
+  if (a.Ksel <= 9) return launch_k<T, NCH, true, 9>(euclid, sampled, a, smem, grid, s);
+  if (a.Ksel <= 16) return launch_k<T, NCH, true, 16>(euclid, sampled, a, smem, grid, s);
+  if (a.Ksel <= 32) return launch_k<T, NCH, true, 32>(euclid, sampled, a, smem, grid, s);
   return CNNA_ERR_K_RANGE;
 }
 
@@ -321,14 +425,23 @@ template <typename T>
 int launch_select_t(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
   if (a.dkp % Mfma<T>::KC != 0 || a.dkp > SelCfg<T>::MAXCH * Mfma<T>::KC || a.dkp % SelCfg<T>::VEC != 0)
     return CNNA_ERR_SHAPE;
+  if (a.Nq > 65536) return CNNA_ERR_SHAPE;
+  const size_t queue = (size_t)QC * NT * (sizeof(float) + sizeof(uint16_t));
+  const int nch0 = a.dkp / Mfma<T>::KC;
+  const bool exact = nch0 == SelCfg<T>::MAXCH / 4 || nch0 == SelCfg<T>::MAXCH / 2 || nch0 == SelCfg<T>::MAXCH;
+  const int kmax = !exact ? 32 : (a.Ksel <= 9 ? 9 : (a.Ksel <= 16 ? 16 : 32));
+  const size_t lists = (size_t)kmax * NT * (sizeof(float) + sizeof(uint16_t));
   const size_t smem = 2 * TJ * (a.dkp + SelCfg<T>::VEC) * sizeof(T) + 2 * TJ * (sizeof(float) + sizeof(int)) +
-                      (size_t)QC * NT * (sizeof(float) + sizeof(int));
+                      queue + lists;
   dim3 grid(a.BH * a.rb_per_bh);
   const int nch = a.dkp / Mfma<T>::KC;
-  const int q = SelCfg<T>::MAXCH / 4;   // chunk classes: d <= 64, 128, 256 (bf16) / 32, 64, 128 (f32)
-  if (nch <= q) return launch_n<T, SelCfg<T>::MAXCH / 4>(euclid, sampled, a, smem, grid, s);
-  if (nch <= 2 * q) return launch_n<T, SelCfg<T>::MAXCH / 2>(euclid, sampled, a, smem, grid, s);
-  return launch_n<T, SelCfg<T>::MAXCH>(euclid, sampled, a, smem, grid, s);
+  constexpr int q = SelCfg<T>::MAXCH / 4;   // head widths 64, 128, 256 (bf16) / 32, 64, 128 (f32)
+  if (nch == q) return launch_n<T, q>(euclid, sampled, a, smem, grid, s);
+  if (nch == 2 * q) return launch_n<T, 2 * q>(euclid, sampled, a, smem, grid, s);
+  if (nch == 4 * q) return launch_n<T, 4 * q>(euclid, sampled, a, smem, grid, s);
+  // other widths: guarded chunks, list of 32
+  if (a.Ksel > 32) return CNNA_ERR_K_RANGE;
+  return launch_k<T, SelCfg<T>::MAXCH, false, 32>(euclid, sampled, a, smem, grid, s);
 }
-}  // namespace
 
+}  // namespace

@@ -118,6 +118,8 @@ class MultiHeadConvNNAttention(nn.Module):
                           self.magnitude_type, self.convolution_type, self.softmax_topk_val,
                           cand is not None, self.coordinate_encoding)
         w0, w1 = self._conv_weights()
-        y = ops.ConvNNCore.apply(x, self.W_q.weight, self.W_k.weight, self.W_v.weight, w0, w1, cand, d)
-        y = self.dropout(y)                                                          # layers.py:316
-        return ops.HeadMergeProj.apply(y, self.W_o.weight, d)
+        z = ops.ConvNNCore.apply(x, self.W_q.weight, self.W_k.weight, self.W_v.weight, w0, w1, cand, d)
+        # dropout on the conv output (layers.py:316); elementwise, so applying it
+        # after the head merge is the same operation on permuted elements
+        z = self.dropout(z)
+        return ops.OutputProj.apply(z, self.W_o.weight, d)

@@ -91,23 +91,29 @@ int cnna_project_qkv(const cnna_desc* d, const void* x, int64_t ldx, const int32
 /* Fused similarity + streaming top-k (layers.py:323-340 then torch.topk in
  * _prime/_prime_softmax/_prime_N/_prime_softmax_N, layers.py:344, 363, 391,
  * 410, with the sampled self mask layers.py:291-292, 304-305).  The N x Nq
- * similarity matrix is never written.  Ties break by lowest candidate index. */
+ * similarity matrix is never written.  Ties break by lowest candidate index.
+ * Also writes the neighbour weights w (softmax of the values, or the raw
+ * values / 1/(value + 1e-8) without softmax) when w is not NULL. */
 int cnna_select(const cnna_desc* d, const void* k, const void* q, const float* kn, const float* qn,
-                const int32_t* cand, int32_t* idx, float* vals, void* stream);
+                const int32_t* cand, int32_t* idx, float* vals, float* w, void* stream);
 
-/* Neighbour weights (softmax / raw / euclidean division), V gather and the
- * Conv1d(kernel=K, stride=K) over the neighbours (layers.py:346-358,
- * 378-386, 393-405, 425-436, 313).
- *   conv_w0: standard (d_k, d_in, K) / depthwise (d_k, 1, K) / dw part (d_in, 1, K)
- *   conv_w1: pointwise (d_k, d_in, 1) for depthwise-separable, else NULL
- *   y (B*H, N, d_k) token-major conv output, dtype of the descriptor */
-int cnna_aggregate(const cnna_desc* d, const void* v, const int32_t* idx, const float* vals,
-                   const void* conv_w0, const void* conv_w1, void* y, void* stream);
+/* V gather and the Conv1d(kernel=K, stride=K) over the neighbours
+ * (layers.py:346-358, 378-386, 393-405, 425-436, 313), then the head merge
+ * (layers.py:316-317, 247-259), producing the tensor that enters W_o.
+ *   w       (B*H, N, K) neighbour weights from cnna_select
+ *   conv_w0 standard (d_k, d_in, K) / depthwise (d_k, 1, K) / dw part (d_in, 1, K)
+ *   conv_w1 pointwise (d_k, d_in, 1) for depthwise-separable, else NULL
+ *   z       (B, N, C) merged:  z[b, t, h*d_k + a] = y[b*H + h][f] with f = a*N + t
+ *           over the token-major flat conv output y (H == 1: a transpose)
+ *   ws      cnna_aggregate_workspace(d) bytes (0 for depthwise) */
+size_t cnna_aggregate_workspace(const cnna_desc* d);
+int cnna_aggregate(const cnna_desc* d, const void* v, const int32_t* idx, const float* w,
+                   const void* conv_w0, const void* conv_w1, void* z, void* ws, size_t ws_bytes,
+                   void* stream);
 
-/* Head merge (layers.py:316-317, 247-259) fused into the A-operand load of
- * the output projection W_o (layers.py:320):  out = merge(y) @ Wo^T.
+/* Output projection W_o (layers.py:320):  out = z @ Wo^T.
  *   out (B, N, C) with row stride ldo elements */
-int cnna_output_proj(const cnna_desc* d, const void* y, const void* Wo, void* out, int64_t ldo,
+int cnna_output_proj(const cnna_desc* d, const void* z, const void* Wo, void* out, int64_t ldo,
                      void* stream);
 
 /* Bytes of workspace cnna_forward needs for this descriptor. */

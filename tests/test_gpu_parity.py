@@ -62,12 +62,12 @@ def run_stages(cfg, p, x, cand):
     cg = None if cand is None else cand.to(torch.int32).to(DEV)
     xg = x.to(DEV)
     q, k, v, qn, kn = ops.project_qkv(d, xg, cg, gpu(p.W_q), gpu(p.W_k), gpu(p.W_v))
-    idx, vals = ops.select(d, k, q, kn, qn, cg)
-    y = ops.aggregate(d, v, idx, vals, gpu(p.conv0), gpu(p.conv1))
-    out = ops.output_proj(d, y, gpu(p.W_o))
+    idx, vals, w = ops.select(d, k, q, kn, qn, cg)
+    z = ops.aggregate(d, v, idx, w, gpu(p.conv0), gpu(p.conv1))
+    out = ops.output_proj(d, z, gpu(p.W_o))
     torch.cuda.synchronize()
-    return d, dict(q=q.cpu(), k=k.cpu(), v=v.cpu(), idx=idx.cpu().long(), vals=vals.cpu(), y=y.cpu(),
-                   out=out.cpu())
+    return d, dict(q=q.cpu(), k=k.cpu(), v=v.cpu(), idx=idx.cpu().long(), vals=vals.cpu(), w=w.cpu(),
+                   z=z.cpu(), out=out.cpu())
 
 
 def check_select(cfg, r, cand, B):
@@ -139,7 +139,7 @@ def test_select_ties_break_by_lowest_index():
     q = torch.zeros(1, N, 16)
     q[..., 0] = 0.5
     q[0, 40, 0] = 0.75          # one clear winner
-    idx, vals = ops.select(d, k.to(DEV), q.to(DEV))
+    idx, vals, _ = ops.select(d, k.to(DEV), q.to(DEV))
     torch.cuda.synchronize()
     exp = [40, 0, 1, 2, 3, 4, 5]
     assert (idx.cpu()[0] == torch.tensor(exp, dtype=torch.int32)).all()
@@ -166,8 +166,10 @@ def test_aggregate_and_merge(name, kw, B, N, dtype):
     d, r = run_stages(cfg, p, x, cand)
     # aggregate on the kernel's own v / idx / vals
     z_exp = O.aggregate_exact(r["v"], r["idx"], r["vals"], p, cfg, B, cand is not None)
-    y = r["y"].double()                                             # (BH, N, dk) token-major
-    z_got = O.head_merge(y.transpose(1, 2), B, cfg.num_heads, cfg.seq_length)
+    z_got = r["z"].double()
+    # the weights the select kernel emitted
+    w_exp = O.neighbour_weights(r["vals"].double(), cfg, cand is not None)
+    torch.testing.assert_close(r["w"].double(), w_exp, rtol=1e-5, atol=1e-6)
     if dtype == torch.float32:
         torch.testing.assert_close(z_got, z_exp, rtol=1e-4, atol=1e-5)
     else:
