@@ -33,6 +33,18 @@ class Desc(ctypes.Structure):
         "softmax", "sampled", "coord")]
 
 
+class Saved(ctypes.Structure):
+    """Mirror of ``cnna_saved``."""
+
+    _fields_ = [(n, ctypes.c_void_p) for n in ("q", "k", "v", "qn", "kn", "idx", "vals", "w")]
+
+
+class Grads(ctypes.Structure):
+    """Mirror of ``cnna_grads``."""
+
+    _fields_ = [(n, ctypes.c_void_p) for n in ("dx", "dWq", "dWk", "dWv", "dconv_w0", "dconv_w1")]
+
+
 def _load():
     if not os.path.exists(LIB_PATH):
         raise ImportError(
@@ -53,6 +65,11 @@ def _load():
         "cnna_output_proj": ([D, P, P, P, I64, P], I32),
         "cnna_forward_workspace": ([D], ctypes.c_size_t),
         "cnna_forward": ([D, P, I64, P, P, P, P, P, P, P, P, I64, P, ctypes.c_size_t, P], I32),
+        "cnna_output_proj_backward_workspace": ([D], ctypes.c_size_t),
+        "cnna_output_proj_backward": ([D, P, P, P, I64, P, P, P, ctypes.c_size_t, P], I32),
+        "cnna_core_backward_workspace": ([D], ctypes.c_size_t),
+        "cnna_core_backward": ([D, P, I64, P, P, P, P, P, P, ctypes.POINTER(Saved), P,
+                                ctypes.POINTER(Grads), P, ctypes.c_size_t, P], I32),
     }
     for name, (args, res) in sigs.items():
         f = getattr(lib, name)
@@ -64,8 +81,9 @@ def _load():
 LIB = _load()
 EXPORTED = ("cnna_abi_version", "cnna_error_string", "cnna_check_desc", "cnna_head_stride",
             "cnna_project_qkv", "cnna_select", "cnna_aggregate_workspace", "cnna_aggregate",
-            "cnna_output_proj",
-            "cnna_forward_workspace", "cnna_forward")
+            "cnna_output_proj", "cnna_forward_workspace", "cnna_forward",
+            "cnna_output_proj_backward_workspace", "cnna_output_proj_backward",
+            "cnna_core_backward_workspace", "cnna_core_backward")
 
 
 def check(status: int) -> None:
@@ -123,7 +141,8 @@ def project_qkv(d: Desc, x: torch.Tensor, cand: Optional[torch.Tensor], Wq, Wk, 
     k = torch.empty((BH, d.N, dkp), dtype=x.dtype, device=x.device)
     v = torch.empty((BH, d.N, dkp), dtype=x.dtype, device=x.device)
     qn = kn = None
-    if d.metric == METRICS["euclidean"]:
+    if d.metric != METRICS["matmul"]:
+        # euclidean distances need the norms; the cosine backward needs them too
         qn = torch.empty((BH * d.Nq,), dtype=torch.float32, device=x.device)
         kn = torch.empty((BH * d.N,), dtype=torch.float32, device=x.device)
     check(LIB.cnna_project_qkv(ctypes.byref(d), _ptr(x), ldx, _ptr(cand), _ptr(Wq.contiguous()),
@@ -177,25 +196,82 @@ def forward_fused(d: Desc, x, cand, Wq, Wk, Wv, Wo, w0, w1=None):
     return out
 
 
+def output_proj_backward(d: Desc, z, Wo, dout):
+    """dz = dout @ Wo, dWo = dout^T @ z."""
+    dout = dout.contiguous()
+    dz = torch.empty_like(z)
+    dWo = torch.empty_like(Wo)
+    nws = LIB.cnna_output_proj_backward_workspace(ctypes.byref(d))
+    ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=z.device)
+    check(LIB.cnna_output_proj_backward(ctypes.byref(d), _ptr(z.contiguous()), _ptr(Wo.contiguous()),
+                                        _ptr(dout), d.C, _ptr(dz), _ptr(dWo), _ptr(ws), nws,
+                                        _stream()))
+    return dz, dWo
+
+
+def core_backward(d: Desc, x, cand, Wq, Wk, Wv, w0, w1, saved, dz):
+    """Gradients of x, W_q, W_k, W_v and the conv weights from dz (B, N, C).
+
+    ``saved`` = (q, k, v, qn, kn, idx, vals, w) from the forward stages.
+    """
+    q, k, v, qn, kn, idx, vals, w = saved
+    x = x.contiguous()
+    dz = dz.contiguous()
+    w0c = w0.to(x.dtype).contiguous()
+    w1c = None if w1 is None else w1.to(x.dtype).contiguous()
+    dx = torch.empty_like(x)
+    dWq, dWk, dWv = (torch.empty(W.shape, dtype=x.dtype, device=x.device) for W in (Wq, Wk, Wv))
+    dw0 = torch.empty(w0.shape, dtype=x.dtype, device=x.device)
+    dw1 = None if w1 is None else torch.empty(w1.shape, dtype=x.dtype, device=x.device)
+    sv = Saved(*(None if t is None else t.data_ptr() for t in (q, k, v, qn, kn, idx, vals, w)))
+    gr = Grads(*(None if t is None else t.data_ptr() for t in (dx, dWq, dWk, dWv, dw0, dw1)))
+    nws = LIB.cnna_core_backward_workspace(ctypes.byref(d))
+    ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=x.device)
+    check(LIB.cnna_core_backward(ctypes.byref(d), _ptr(x), x.stride(1), _ptr(cand),
+                                 _ptr(Wq.contiguous()), _ptr(Wk.contiguous()), _ptr(Wv.contiguous()),
+                                 _ptr(w0c), _ptr(w1c), ctypes.byref(sv), _ptr(dz), ctypes.byref(gr),
+                                 _ptr(ws), nws, _stream()))
+    return dx, dWq, dWk, dWv, dw0, dw1
+
+
 # --------------------------------------------------------------------------
 # autograd
 # --------------------------------------------------------------------------
 
 class ConvNNCore(torch.autograd.Function):
-    """x -> z (B, N, C): projections, neighbour selection, aggregation, head merge."""
+    """x -> z (B, N, C): projections, neighbour selection, aggregation, head merge.
+
+    ``reference_errors``: raise where the reference's autograd raises.  The
+    reference masks the self column of the sampled euclidean distance matrix in
+    place on the output of ``sqrt`` (layers.py:278, 291-292, 304-305), so its
+    backward fails with RuntimeError for sampled euclidean; the kernels here
+    can differentiate that case, and do when this flag is off.
+    """
 
     @staticmethod
-    def forward(ctx, x, Wq, Wk, Wv, w0, w1, cand, d):
+    def forward(ctx, x, Wq, Wk, Wv, w0, w1, cand, d, reference_errors=False):
         q, k, v, qn, kn = project_qkv(d, x, cand, Wq, Wk, Wv)
         idx, vals, w = select(d, k, q, kn, qn, cand)
         z = aggregate(d, v, idx, w, w0, w1)
         ctx.d = d
-        ctx.save_for_backward(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, idx, vals, w)
+        ctx.reference_errors = reference_errors
+        ctx.save_for_backward(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w)
         return z
 
     @staticmethod
     def backward(ctx, dz):
-        raise NotImplementedError("cnna: backward kernels are not built yet")
+        d = ctx.d
+        if ctx.reference_errors and d.sampled and d.metric == METRICS["euclidean"]:
+            raise RuntimeError(
+                "one of the variables needed for gradient computation has been modified by an "
+                "inplace operation: the sampled euclidean similarity is masked in place after "
+                "sqrt (layers.py:291-292, 304-305)")
+        x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w = ctx.saved_tensors
+        dx, dWq, dWk, dWv, dw0, dw1 = core_backward(ctx.d, x, cand, Wq, Wk, Wv, w0, w1,
+                                                    (q, k, v, qn, kn, idx, vals, w), dz)
+        dw0 = dw0.to(w0.dtype)
+        dw1 = None if dw1 is None else dw1.to(w1.dtype)
+        return dx, dWq, dWk, dWv, dw0, dw1, None, None, None
 
 
 class OutputProj(torch.autograd.Function):
@@ -209,4 +285,6 @@ class OutputProj(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout):
-        raise NotImplementedError("cnna: backward kernels are not built yet")
+        z, Wo = ctx.saved_tensors
+        dz, dWo = output_proj_backward(ctx.d, z, Wo, dout)
+        return dz, dWo, None

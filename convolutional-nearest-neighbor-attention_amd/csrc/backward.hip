@@ -1,0 +1,681 @@
+// Backward kernels of the operator (autograd of layers.py:261-450).
+//
+// The reference differentiates a dense (BH, N, Nq) similarity matrix; here the
+// similarity gradient is nonzero only at the K selected entries of each row,
+// so every stage works on the (BH, N, K) neighbour lists:
+//
+//   tok_bwd     per token i: dw[i, r] = sum_c dP[c, i, r] * v[c, idx[i, r]],
+//               softmax / weight backward -> dS[i, r], stored as a coefficient
+//               coef = dS * (1/sqrt(d_k) | 1 | 1/s) per metric, and the key
+//               gradient dk_i = sum_r coef * q_col(r) (+ normalisation /
+//               distance terms); depthwise weight partial sums.
+//   csr_*       reverse adjacency of the lists (count, scan, fill, sort by
+//               entry id), so that
+//   pull        dv_j = sum over entries reading v_j of w * dP and
+//               dq_j = sum over entries selecting column j of coef * k_i
+//               are summed in a fixed order (no floating-point atomics).
+//
+// dP (gradient of the gathered input prime) is W0[c, r] * g[c, i] for the
+// depthwise conv and the depthwise stage of the separable conv, and a
+// materialised GEMM result for the standard conv.
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+CNNA_DEV float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+// CPL consecutive channels starting at c0 of a row; zero beyond lim.
+template <typename T, int CPL> struct Row;
+template <> struct Row<uint16_t, 1> {
+  static CNNA_DEV void load(const uint16_t* p, float (&o)[1]) { o[0] = bf2f(*p); }
+};
+template <> struct Row<uint16_t, 2> {
+  static CNNA_DEV void load(const uint16_t* p, float (&o)[2]) {
+    const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
+    o[0] = __uint_as_float(u << 16);
+    o[1] = __uint_as_float(u & 0xffff0000u);
+  }
+};
+template <> struct Row<uint16_t, 4> {
+  static CNNA_DEV void load(const uint16_t* p, float (&o)[4]) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    o[0] = __uint_as_float(u.x << 16);
+    o[1] = __uint_as_float(u.x & 0xffff0000u);
+    o[2] = __uint_as_float(u.y << 16);
+    o[3] = __uint_as_float(u.y & 0xffff0000u);
+  }
+};
+template <> struct Row<float, 1> {
+  static CNNA_DEV void load(const float* p, float (&o)[1]) { o[0] = *p; }
+};
+template <> struct Row<float, 2> {
+  static CNNA_DEV void load(const float* p, float (&o)[2]) {
+    const float2 u = *reinterpret_cast<const float2*>(p);
+    o[0] = u.x;
+    o[1] = u.y;
+  }
+};
+template <> struct Row<float, 4> {
+  static CNNA_DEV void load(const float* p, float (&o)[4]) {
+    const float4 u = *reinterpret_cast<const float4*>(p);
+    o[0] = u.x; o[1] = u.y; o[2] = u.z; o[3] = u.w;
+  }
+};
+
+template <typename T, int CPL>
+CNNA_DEV void load_row(const T* row, int c0, int lim, bool vec, float (&o)[CPL]) {
+  if (vec && c0 + CPL <= lim) {
+    Row<T, CPL>::load(row + c0, o);
+  } else {
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) o[u] = (c0 + u < lim) ? ldf(row + c0 + u) : 0.0f;
+  }
+}
+
+// channels [c0, c0 + CPL) below dk into an unsplit (rows, C) destination
+template <typename T, int CPL>
+CNNA_DEV void store_row(T* row, int c0, int dk, const float (&o)[CPL]) {
+#pragma unroll
+  for (int u = 0; u < CPL; ++u)
+    if (c0 + u < dk) stf(row + c0 + u, o[u]);
+}
+
+// ------------------------------------------------------------------ unmerge
+// Inverse of the head merge Z[b, t, h*dk + a] = y_bh[a*N + t] (H > 1) and of
+// the transpose Z[b, i, c] = y_b[i*dk + c] (H == 1), y_bh flat token-major.
+template <typename T>
+__global__ __launch_bounds__(256) void unmerge_kernel(const T* dz, T* dy, int BH, int N, int dk,
+                                                      int H, int C) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per = (int64_t)N * dk;
+  if (e >= (int64_t)BH * per) return;
+  const int bh = (int)(e / per);
+  const int64_t f = e - (int64_t)bh * per;
+  const int b = bh / H, h = bh - b * H;
+  int64_t src;
+  if (H == 1) {
+    src = (int64_t)b * N * C + f;
+  } else {
+    const int a = (int)(f / N), t = (int)(f - (int64_t)a * N);
+    src = ((int64_t)b * N + t) * C + h * dk + a;
+  }
+  dy[e] = dz[src];
+}
+
+// ------------------------------------------------------------------ gather P
+template <typename T>
+__global__ __launch_bounds__(256) void gather_p_kernel(const T* v, const int32_t* idx,
+                                                       const float* w, T* P, int BH, int N, int K,
+                                                       int din, int dkp) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;   // over BH*N*K*din
+  const int64_t tot = (int64_t)BH * N * K * din;
+  if (e >= tot) return;
+  const int64_t ent = e / din;              // (bh*N + i)*K + r
+  const int c = (int)(e - ent * din);
+  const int64_t tok = ent / K;
+  const int bh = (int)(tok / N);
+  const int j = idx[ent];
+  stf(P + e, w[ent] * ldf(v + ((int64_t)bh * N + j) * dkp + c));
+}
+
+// ------------------------------------------------------------------ tok_bwd
+template <typename T, int CPL, int KMAX, bool DW>
+__global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
+  constexpr int CW = 64 * CPL;
+  __shared__ float sW[DW ? KMAX * CW : 1];   // W0 as [r][c]; reused for the block reduction
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int c0 = lane * CPL;
+  const int K = a.K;
+  if (DW) {
+    const T* W0 = static_cast<const T*>(a.w0);
+    for (int e = tid; e < KMAX * CW; e += 256) {
+      const int r = e / CW, c = e - r * CW;
+      sW[e] = (r < K && c < a.din) ? ldf(W0 + c * K + r) : 0.0f;
+    }
+    __syncthreads();
+  }
+  float acc[DW ? KMAX : 1][CPL];
+#pragma unroll
+  for (int r = 0; r < (DW ? KMAX : 1); ++r)
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) acc[r][u] = 0.0f;
+
+  const bool euc = a.metric == CNNA_EUCLIDEAN, cos_ = a.metric == CNNA_COSINE;
+  const bool gvec = (a.din % CPL) == 0;
+  const int ntok = a.BH * a.N;
+  const int nw = gridDim.x * 4;
+  for (int tok = blockIdx.x * 4 + wv; tok < ntok; tok += nw) {
+    const int bh = tok / a.N, i = tok - bh * a.N;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int64_t ebase = (int64_t)tok * K;
+    const bool valid = lane < K;
+    int my_j = 0;
+    float my_w = 0.0f, my_val = 0.0f;
+    if (valid) {
+      my_j = a.idx[ebase + lane];
+      my_w = a.w[ebase + lane];
+      my_val = a.vals[ebase + lane];
+    }
+    const T* V = static_cast<const T*>(a.v) + (int64_t)bh * a.N * a.dkp;
+    float gv[CPL];
+    if (DW) load_row<T, CPL>(static_cast<const T*>(a.g) + (int64_t)tok * a.din, c0, a.din, gvec, gv);
+
+    // dw[r] = sum_c dP[c, r] * v[c, idx[r]]
+    float my_dw = 0.0f;
+#pragma unroll
+    for (int r = 0; r < KMAX; ++r) {
+      if (r < K) {
+        const int t = __shfl(my_j, r);
+        float vv[CPL];
+        load_row<T, CPL>(V + (int64_t)t * a.dkp, c0, a.dkp, true, vv);
+        float p = 0.0f;
+        if (DW) {
+          const float wr = __shfl(my_w, r);
+#pragma unroll
+          for (int u = 0; u < CPL; ++u) {
+            const float pr = gv[u] * vv[u];
+            acc[DW ? r : 0][u] += wr * pr;
+            p += sW[(DW ? r : 0) * CW + c0 + u] * pr;
+          }
+        } else {
+          float dp[CPL];
+          load_row<T, CPL>(static_cast<const T*>(a.dP) + (ebase + r) * a.din, c0, a.din, gvec, dp);
+#pragma unroll
+          for (int u = 0; u < CPL; ++u) p += dp[u] * vv[u];
+        }
+        p = wave_sum(p);
+        if (lane == r) my_dw = p;
+      }
+    }
+
+    // weight backward -> dS (layers.py:342-437)
+    float ds;
+    if (a.softmax) {
+      const float dot = wave_sum(valid ? my_w * my_dw : 0.0f);
+      ds = my_w * (my_dw - dot);
+      if (euc) ds = -ds;                       // softmax(-vals)
+    } else if (euc) {
+      const float den = my_val + 1e-8f;        // prime / (vals + 1e-8)
+      ds = -my_dw / (den * den);
+    } else {
+      ds = my_dw;                              // vals * prime
+    }
+    // sampled: slot 0 is the constant self logit, a masked column is constant
+    if (a.sampled && (lane == 0 || my_j == i)) ds = 0.0f;
+    if (!valid) ds = 0.0f;
+    float coef = ds;
+    if (a.metric == CNNA_MATMUL) coef = ds * a.scale;
+    else if (euc) coef = (ds == 0.0f) ? 0.0f : ds / my_val;   // d sqrt(d2) = 1/(2s) * d d2
+    if (valid) a.coef[ebase + lane] = coef;
+    int my_col = my_j;
+    if (a.sampled) my_col = (valid && coef != 0.0f) ? min(max(a.inv[my_j], 0), a.Nq - 1) : 0;
+
+    // dk_i = sum_r coef[r] * q[col(r)]  (+ metric terms)
+    float dk[CPL];
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) dk[u] = 0.0f;
+    const T* Q = static_cast<const T*>(a.q) + (int64_t)bh * a.Nq * a.dkp;
+#pragma unroll
+    for (int r = 0; r < KMAX; ++r) {
+      if (r < K) {
+        const float cr = __shfl(coef, r);
+        if (cr != 0.0f) {
+          const int col = __shfl(my_col, r);
+          float qv[CPL];
+          load_row<T, CPL>(Q + (int64_t)col * a.dkp, c0, a.dkp, true, qv);
+#pragma unroll
+          for (int u = 0; u < CPL; ++u) dk[u] += cr * qv[u];
+        }
+      }
+    }
+    if (cos_ || euc) {
+      float kv[CPL];
+      load_row<T, CPL>(static_cast<const T*>(a.k) + (int64_t)tok * a.dkp, c0, a.dkp, true, kv);
+      if (cos_) {
+        // F.normalize backward: (dkh - kh (kh . dkh)) / max(|k|, eps)
+        float d = 0.0f;
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) d += kv[u] * dk[u];
+        d = wave_sum(d);
+        const float nrm = sqrtf(a.kn[tok]);
+#pragma unroll
+        for (int u = 0; u < CPL; ++u)
+          dk[u] = nrm > 1e-12f ? (dk[u] - kv[u] * d) / nrm : dk[u] / 1e-12f;
+      } else {
+        // d/dk sqrt(|k|^2 + |q|^2 - 2 k.q) summed: k * sum(coef) - sum(coef * q)
+        const float cs = wave_sum(coef);
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) dk[u] = kv[u] * cs - dk[u];
+      }
+    }
+    T* dst = static_cast<T*>(a.dst) + ((int64_t)b * a.N + i) * a.ldd + a.offd + h * a.dk;
+    store_row<T, CPL>(dst, c0, a.dk, dk);
+  }
+
+  if (DW) {
+    // block partial of dW0[c, r] = sum_tokens w[r] g[c] v[c, idx[r]], waves added in order
+    __syncthreads();
+    for (int w = 0; w < 4; ++w) {
+      if (wv == w) {
+#pragma unroll
+        for (int r = 0; r < KMAX; ++r)
+#pragma unroll
+          for (int u = 0; u < CPL; ++u) {
+            float* p = &sW[(DW ? r : 0) * CW + c0 + u];
+            *p = (w == 0 ? 0.0f : *p) + acc[DW ? r : 0][u];
+          }
+      }
+      __syncthreads();
+    }
+    float* out = a.w0part + (int64_t)blockIdx.x * a.din * K;
+    for (int e = tid; e < a.din * K; e += 256) {
+      const int c = e / K, r = e - c * K;
+      out[e] = sW[r * CW + c];
+    }
+  }
+}
+
+template <typename T, int CPL, int KMAX>
+int launch_tok_t(const TokBwdArgs& a, hipStream_t s) {
+  dim3 grid(a.nblk);
+  if (a.std_conv)
+    hipLaunchKernelGGL((tok_bwd_kernel<T, CPL, KMAX, false>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((tok_bwd_kernel<T, CPL, KMAX, true>), grid, dim3(256), 0, s, a);
+  return (int)hipGetLastError();
+}
+
+template <typename T, int CPL>
+int launch_tok_k(const TokBwdArgs& a, hipStream_t s) {
+  if (a.K <= 16) return launch_tok_t<T, CPL, 16>(a, s);
+  if (a.K <= 32) return launch_tok_t<T, CPL, 32>(a, s);
+  return CNNA_ERR_K_RANGE;
+}
+
+template <typename T>
+int launch_tok_c(const TokBwdArgs& a, hipStream_t s) {
+  if (a.dkp <= 64) return launch_tok_k<T, 1>(a, s);
+  if (a.dkp <= 128) return launch_tok_k<T, 2>(a, s);
+  if (a.dkp <= 256) return launch_tok_k<T, 4>(a, s);
+  return CNNA_ERR_SHAPE;
+}
+
+__global__ __launch_bounds__(256) void w0_reduce_f32(const float* part, int nblk, int n, float* out) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= n) return;
+  float acc = 0.0f;
+  for (int b = 0; b < nblk; ++b) acc += part[(int64_t)b * n + e];
+  out[e] = acc;
+}
+__global__ __launch_bounds__(256) void w0_reduce_bf16(const float* part, int nblk, int n,
+                                                      uint16_t* out) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= n) return;
+  float acc = 0.0f;
+  for (int b = 0; b < nblk; ++b) acc += part[(int64_t)b * n + e];
+  out[e] = f2bf(acc);
+}
+
+// ------------------------------------------------------------------ CSR
+CNNA_DEV int entry_key(const CsrArgs& c, int64_t ge, int i, int r) {
+  const int j = c.idx[ge];
+  if (c.mode == CSR_TOKEN) return j;
+  if (r == 0 || j == i) return -1;             // self slot / masked column
+  const int col = c.inv[j];
+  return col < c.nkeys ? col : -1;
+}
+
+__global__ __launch_bounds__(256) void csr_count_kernel(CsrArgs c) {
+  const int64_t ge = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t NK = (int64_t)c.N * c.K;
+  if (ge >= (int64_t)c.BH * NK) return;
+  const int bh = (int)(ge / NK);
+  const int e = (int)(ge - (int64_t)bh * NK);
+  const int i = e / c.K, r = e - i * c.K;
+  const int key = entry_key(c, ge, i, r);
+  if (key >= 0) atomicAdd(&c.cnt[(int64_t)bh * c.nkeys + key], 1);
+}
+
+// one block per (b, h): exclusive scan of the counts; counts reset to 0 (fill cursors)
+__global__ __launch_bounds__(1024) void csr_scan_kernel(CsrArgs c) {
+  __shared__ int part[1024];
+  const int bh = blockIdx.x, tid = threadIdx.x;
+  int32_t* cnt = c.cnt + (int64_t)bh * c.nkeys;
+  int32_t* off = c.off + (int64_t)bh * (c.nkeys + 1);
+  const int per = (c.nkeys + 1023) / 1024;
+  const int k0 = tid * per, k1 = min(c.nkeys, k0 + per);
+  int s = 0;
+  for (int k = k0; k < k1; ++k) s += cnt[k];
+  part[tid] = s;
+  __syncthreads();
+  for (int d = 1; d < 1024; d <<= 1) {
+    const int x = tid >= d ? part[tid - d] : 0;
+    __syncthreads();
+    part[tid] += x;
+    __syncthreads();
+  }
+  int run = part[tid] - s;
+  for (int k = k0; k < k1; ++k) {
+    off[k] = run;
+    run += cnt[k];
+    cnt[k] = 0;
+  }
+  if (tid == 1023) off[c.nkeys] = part[1023];
+}
+
+__global__ __launch_bounds__(256) void csr_fill_kernel(CsrArgs c) {
+  const int64_t ge = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t NK = (int64_t)c.N * c.K;
+  if (ge >= (int64_t)c.BH * NK) return;
+  const int bh = (int)(ge / NK);
+  const int e = (int)(ge - (int64_t)bh * NK);
+  const int i = e / c.K, r = e - i * c.K;
+  const int key = entry_key(c, ge, i, r);
+  if (key < 0) return;
+  const int pos = atomicAdd(&c.cnt[(int64_t)bh * c.nkeys + key], 1);
+  c.tmp[(int64_t)bh * NK + c.off[(int64_t)bh * (c.nkeys + 1) + key] + pos] = e;
+}
+
+// one wave per key: rank sort of the bucket (entry ids are distinct)
+constexpr int SORT_LDS = 1024;
+__global__ __launch_bounds__(256) void csr_sort_kernel(CsrArgs c) {
+  __shared__ int buf[4][SORT_LDS];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + wv;
+  if (gw >= (int64_t)c.BH * c.nkeys) return;
+  const int bh = (int)(gw / c.nkeys), key = (int)(gw - (int64_t)bh * c.nkeys);
+  const int64_t NK = (int64_t)c.N * c.K;
+  const int32_t* off = c.off + (int64_t)bh * (c.nkeys + 1);
+  const int beg = off[key], n = off[key + 1] - beg;
+  const int32_t* src = c.tmp + bh * NK + beg;
+  int32_t* dst = c.list + bh * NK + beg;
+  if (n <= SORT_LDS) {
+    for (int x = lane; x < n; x += 64) buf[wv][x] = src[x];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    for (int x = lane; x < n; x += 64) {
+      const int me = buf[wv][x];
+      int rank = 0;
+      for (int y = 0; y < n; ++y) rank += buf[wv][y] < me;
+      dst[rank] = me;
+    }
+  } else {
+    for (int x = lane; x < n; x += 64) {
+      const int me = src[x];
+      int rank = 0;
+      for (int y = 0; y < n; ++y) rank += src[y] < me;
+      dst[rank] = me;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e < n) p[e] = v;
+}
+
+__global__ __launch_bounds__(256) void inv_map_kernel(const int32_t* cand, int Nq, int N,
+                                                      int32_t* inv) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= Nq) return;
+  const int t = cand[j];
+  if (t >= 0 && t < N) atomicMin(&inv[t], j);
+}
+
+// ------------------------------------------------------------------ pull
+template <typename T, int CPL>
+__global__ __launch_bounds__(256) void pull_kernel(PullArgs a) {
+  constexpr int CW = 64 * CPL;
+  extern __shared__ float sW[];                   // depthwise: W0 as [r][c]
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int c0 = lane * CPL;
+  const bool dwv = a.do_v && !a.std_conv;
+  if (dwv) {
+    const T* W0 = static_cast<const T*>(a.w0);
+    for (int e = tid; e < a.K * CW; e += 256) {
+      const int r = e / CW, c = e - r * CW;
+      sW[e] = c < a.din ? ldf(W0 + c * a.K + r) : 0.0f;
+    }
+    __syncthreads();
+  }
+  const int64_t gw = (int64_t)blockIdx.x * 4 + wv;
+  if (gw >= (int64_t)a.BH * a.nkeys) return;
+  const int bh = (int)(gw / a.nkeys), key = (int)(gw - (int64_t)bh * a.nkeys);
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int64_t NK = (int64_t)a.N * a.K;
+  const int32_t* off = a.off + (int64_t)bh * (a.nkeys + 1);
+  const int beg = off[key], end = off[key + 1];
+  const int32_t* list = a.list + bh * NK;
+  const bool gvec = (a.din % CPL) == 0;
+  const T* G = static_cast<const T*>(a.g);
+  const T* DP = static_cast<const T*>(a.dP);
+  const T* Kt = static_cast<const T*>(a.k) + (int64_t)bh * a.N * a.dkp;
+
+  float dv[CPL], dq[CPL], cs = 0.0f;
+#pragma unroll
+  for (int u = 0; u < CPL; ++u) dv[u] = dq[u] = 0.0f;
+  for (int x = beg; x < end; ++x) {
+    const int e = list[x];
+    const int i = e / a.K, r = e - i * a.K;
+    if (a.do_v) {
+      const float we = a.w[bh * NK + e];
+      float gg[CPL];
+      if (a.std_conv) {
+        load_row<T, CPL>(DP + (bh * NK + e) * a.din, c0, a.din, gvec, gg);
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) dv[u] += we * gg[u];
+      } else {
+        load_row<T, CPL>(G + ((int64_t)bh * a.N + i) * a.din, c0, a.din, gvec, gg);
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) dv[u] += we * (sW[r * CW + c0 + u] * gg[u]);
+      }
+    }
+    if (a.do_q) {
+      const float ce = a.coef[bh * NK + e];
+      if (ce != 0.0f) {
+        float kk[CPL];
+        load_row<T, CPL>(Kt + (int64_t)i * a.dkp, c0, a.dkp, true, kk);
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) dq[u] += ce * kk[u];
+        cs += ce;
+      }
+    }
+  }
+  if (a.do_v) {
+    T* dst = static_cast<T*>(a.dst_v) + ((int64_t)b * a.N + key) * a.ld_v + a.off_v + h * a.dk;
+    store_row<T, CPL>(dst, c0, a.dk, dv);
+  }
+  if (a.do_q) {
+    if (a.metric != CNNA_MATMUL) {
+      float qv[CPL];
+      load_row<T, CPL>(static_cast<const T*>(a.q) + ((int64_t)bh * a.nkeys + key) * a.dkp, c0,
+                       a.dkp, true, qv);
+      if (a.metric == CNNA_COSINE) {
+        float d = 0.0f;
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) d += qv[u] * dq[u];
+        d = wave_sum(d);
+        const float nrm = sqrtf(a.qn[(int64_t)bh * a.nkeys + key]);
+#pragma unroll
+        for (int u = 0; u < CPL; ++u)
+          dq[u] = nrm > 1e-12f ? (dq[u] - qv[u] * d) / nrm : dq[u] / 1e-12f;
+      } else {
+        // q * sum(coef) - sum(coef * k)
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) dq[u] = qv[u] * cs - dq[u];
+      }
+    }
+    T* dst = static_cast<T*>(a.dst_q) + ((int64_t)b * a.nkeys + key) * a.ld_q + a.off_q + h * a.dk;
+    store_row<T, CPL>(dst, c0, a.dk, dq);
+  }
+}
+
+template <typename T>
+int launch_pull_t(const PullArgs& a, hipStream_t s) {
+  const int64_t waves = (int64_t)a.BH * a.nkeys;
+  if (waves <= 0) return 0;
+  dim3 grid((unsigned)((waves + 3) / 4));
+  auto lds = [&](int cpl) { return (size_t)((a.do_v && !a.std_conv) ? a.K * 64 * cpl * 4 : 0); };
+  if (a.dkp <= 64)
+    hipLaunchKernelGGL((pull_kernel<T, 1>), grid, dim3(256), lds(1), s, a);
+  else if (a.dkp <= 128)
+    hipLaunchKernelGGL((pull_kernel<T, 2>), grid, dim3(256), lds(2), s, a);
+  else if (a.dkp <= 256)
+    hipLaunchKernelGGL((pull_kernel<T, 4>), grid, dim3(256), lds(4), s, a);
+  else
+    return CNNA_ERR_SHAPE;
+  return (int)hipGetLastError();
+}
+
+// ------------------------------------------------------------------ sampled rows
+template <typename T>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const T* x, int64_t ldx,
+                                                          const int32_t* cand, T* xs, int B, int N,
+                                                          int Nq, int C) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (int64_t)B * Nq * C) return;
+  const int64_t row = e / C;
+  const int c = (int)(e - row * C);
+  const int b = (int)(row / Nq), j = (int)(row - (int64_t)b * Nq);
+  xs[e] = x[((int64_t)b * N + cand[j]) * ldx + c];
+}
+
+// one thread per (b, c): rows added in column order j = 0 .. Nq-1
+template <typename T>
+__global__ __launch_bounds__(256) void scatter_rows_kernel(const T* dxs, const int32_t* cand, T* dx,
+                                                           int B, int N, int Nq, int C) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (int64_t)B * C) return;
+  const int b = (int)(e / C), c = (int)(e - (int64_t)b * C);
+  for (int j = 0; j < Nq; ++j) {
+    T* p = dx + ((int64_t)b * N + cand[j]) * C + c;
+    stf(p, ldf(p) + ldf(dxs + ((int64_t)b * Nq + j) * C + c));
+  }
+}
+
+inline dim3 grid_for(int64_t n) { return dim3((unsigned)((n + 255) / 256)); }
+
+}  // namespace
+
+int launch_unmerge(int dtype, const void* dz, void* dy, int BH, int N, int dk, int H, int C,
+                   hipStream_t s) {
+  const int64_t n = (int64_t)BH * N * dk;
+  if (n <= 0) return 0;
+  if (dtype == CNNA_BF16)
+    hipLaunchKernelGGL(unmerge_kernel<uint16_t>, grid_for(n), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(dz), static_cast<uint16_t*>(dy), BH, N, dk, H, C);
+  else if (dtype == CNNA_F32)
+    hipLaunchKernelGGL(unmerge_kernel<float>, grid_for(n), dim3(256), 0, s,
+                       static_cast<const float*>(dz), static_cast<float*>(dy), BH, N, dk, H, C);
+  else
+    return CNNA_ERR_DTYPE;
+  return (int)hipGetLastError();
+}
+
+int launch_gather_p(int dtype, const void* v, const int32_t* idx, const float* w, void* P, int BH,
+                    int N, int K, int din, int dkp, hipStream_t s) {
+  const int64_t n = (int64_t)BH * N * K * din;
+  if (n <= 0) return 0;
+  if (dtype == CNNA_BF16)
+    hipLaunchKernelGGL(gather_p_kernel<uint16_t>, grid_for(n), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(v), idx, w, static_cast<uint16_t*>(P), BH, N, K,
+                       din, dkp);
+  else if (dtype == CNNA_F32)
+    hipLaunchKernelGGL(gather_p_kernel<float>, grid_for(n), dim3(256), 0, s,
+                       static_cast<const float*>(v), idx, w, static_cast<float*>(P), BH, N, K, din,
+                       dkp);
+  else
+    return CNNA_ERR_DTYPE;
+  return (int)hipGetLastError();
+}
+
+int launch_tok_bwd(int dtype, const TokBwdArgs& a0, hipStream_t s) {
+  if (a0.BH <= 0 || a0.N <= 0) return 0;
+  TokBwdArgs a = a0;
+  a.nblk = tok_bwd_blocks(a.BH, a.N);
+  if (dtype == CNNA_BF16) return launch_tok_c<uint16_t>(a, s);
+  if (dtype == CNNA_F32) return launch_tok_c<float>(a, s);
+  return CNNA_ERR_DTYPE;
+}
+
+int launch_w0_reduce(int dtype, const float* part, int nblk, int n, void* out, hipStream_t s) {
+  if (n <= 0) return 0;
+  if (dtype == CNNA_BF16)
+    hipLaunchKernelGGL(w0_reduce_bf16, grid_for(n), dim3(256), 0, s, part, nblk, n,
+                       static_cast<uint16_t*>(out));
+  else if (dtype == CNNA_F32)
+    hipLaunchKernelGGL(w0_reduce_f32, grid_for(n), dim3(256), 0, s, part, nblk, n,
+                       static_cast<float*>(out));
+  else
+    return CNNA_ERR_DTYPE;
+  return (int)hipGetLastError();
+}
+
+int launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t s) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(fill_i32_kernel, grid_for(n), dim3(256), 0, s, p, n, v);
+  return (int)hipGetLastError();
+}
+
+int launch_inv_map(const int32_t* cand, int Nq, int N, int32_t* inv, hipStream_t s) {
+  int st = launch_fill_i32(inv, N, Nq, s);
+  if (st || Nq <= 0) return st;
+  hipLaunchKernelGGL(inv_map_kernel, grid_for(Nq), dim3(256), 0, s, cand, Nq, N, inv);
+  return (int)hipGetLastError();
+}
+
+int launch_csr(const CsrArgs& c, hipStream_t s) {
+  const int64_t ne = (int64_t)c.BH * c.N * c.K;
+  if (ne <= 0 || c.nkeys <= 0) return 0;
+  int st = launch_fill_i32(c.cnt, (int64_t)c.BH * c.nkeys, 0, s);
+  if (st) return st;
+  hipLaunchKernelGGL(csr_count_kernel, grid_for(ne), dim3(256), 0, s, c);
+  hipLaunchKernelGGL(csr_scan_kernel, dim3(c.BH), dim3(1024), 0, s, c);
+  hipLaunchKernelGGL(csr_fill_kernel, grid_for(ne), dim3(256), 0, s, c);
+  hipLaunchKernelGGL(csr_sort_kernel, dim3((unsigned)(((int64_t)c.BH * c.nkeys + 3) / 4)), dim3(256),
+                     0, s, c);
+  return (int)hipGetLastError();
+}
+
+int launch_pull(int dtype, const PullArgs& p, hipStream_t s) {
+  if (dtype == CNNA_BF16) return launch_pull_t<uint16_t>(p, s);
+  if (dtype == CNNA_F32) return launch_pull_t<float>(p, s);
+  return CNNA_ERR_DTYPE;
+}
+
+int launch_gather_rows(int dtype, const void* x, int64_t ldx, const int32_t* cand, void* xs, int B,
+                       int N, int Nq, int C, hipStream_t s) {
+  const int64_t n = (int64_t)B * Nq * C;
+  if (n <= 0) return 0;
+  if (dtype == CNNA_BF16)
+    hipLaunchKernelGGL(gather_rows_kernel<uint16_t>, grid_for(n), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), ldx, cand, static_cast<uint16_t*>(xs), B, N,
+                       Nq, C);
+  else if (dtype == CNNA_F32)
+    hipLaunchKernelGGL(gather_rows_kernel<float>, grid_for(n), dim3(256), 0, s,
+                       static_cast<const float*>(x), ldx, cand, static_cast<float*>(xs), B, N, Nq, C);
+  else
+    return CNNA_ERR_DTYPE;
+  return (int)hipGetLastError();
+}
+
+int launch_scatter_rows(int dtype, const void* dxs, const int32_t* cand, void* dx, int B, int N,
+                        int Nq, int C, hipStream_t s) {
+  const int64_t n = (int64_t)B * C;
+  if (n <= 0 || Nq <= 0) return 0;
+  if (dtype == CNNA_BF16)
+    hipLaunchKernelGGL(scatter_rows_kernel<uint16_t>, grid_for(n), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(dxs), cand, static_cast<uint16_t*>(dx), B, N, Nq,
+                       C);
+  else if (dtype == CNNA_F32)
+    hipLaunchKernelGGL(scatter_rows_kernel<float>, grid_for(n), dim3(256), 0, s,
+                       static_cast<const float*>(dxs), cand, static_cast<float*>(dx), B, N, Nq, C);
+  else
+    return CNNA_ERR_DTYPE;
+  return (int)hipGetLastError();
+}

@@ -8,22 +8,9 @@
 #include "common.h"
 #include "kernels.h"
 
-namespace {
+#include "desc_util.h"
 
-int elem_size(int dtype) { return dtype == CNNA_BF16 ? 2 : (dtype == CNNA_F32 ? 4 : 0); }
-
-int din_of(const cnna_desc* d) { return d->C / d->H + (d->coord ? 1 : 0); }
-
-int dkp_of(const cnna_desc* d) {
-  // channels padded to the MFMA reduction depth (16) and 16-byte rows
-  return (int)cnna_round_up((size_t)din_of(d), 16);
-}
-
-int ksel_of(const cnna_desc* d) { return d->sampled ? d->K - 1 : d->K; }
-
-bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
-
-}  // namespace
+using namespace cnna_desc_util;
 
 extern "C" {
 
@@ -124,9 +111,9 @@ int cnna_project_qkv(const cnna_desc* d, const void* x, int64_t ldx, const int32
   p.dkp = dkp;
   p.coord = d->coord;
   if (pad || cos || euc) {
-    p.t = k; p.rows = d->N; p.rows_total = BH * d->N; p.normalize = cos; p.norms = euc ? kn : nullptr;
+    p.t = k; p.rows = d->N; p.rows_total = BH * d->N; p.normalize = cos; p.norms = (euc || cos) ? kn : nullptr;
     if ((st = launch_prep(d->dtype, p, s))) return st;
-    p.t = q; p.rows = d->Nq; p.rows_total = BH * d->Nq; p.normalize = cos; p.norms = euc ? qn : nullptr;
+    p.t = q; p.rows = d->Nq; p.rows_total = BH * d->Nq; p.normalize = cos; p.norms = (euc || cos) ? qn : nullptr;
     if ((st = launch_prep(d->dtype, p, s))) return st;
   }
   if (pad) {

@@ -1,0 +1,33 @@
+// Descriptor-derived sizes shared by the C-ABI translation units.
+#pragma once
+
+#include <stdint.h>
+
+#include "common.h"
+
+namespace cnna_desc_util {
+
+inline int elem_size(int dtype) { return dtype == CNNA_BF16 ? 2 : (dtype == CNNA_F32 ? 4 : 0); }
+
+inline int din_of(const cnna_desc* d) { return d->C / d->H + (d->coord ? 1 : 0); }
+
+// channels padded to the MFMA reduction depth (16) and 16-byte rows
+inline int dkp_of(const cnna_desc* d) { return (int)cnna_round_up((size_t)din_of(d), 16); }
+
+inline int ksel_of(const cnna_desc* d) { return d->sampled ? d->K - 1 : d->K; }
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// bump allocator over a caller workspace (256-byte aligned slices)
+struct Carve {
+  char* p;
+  size_t used = 0;
+  explicit Carve(void* base) : p(static_cast<char*>(base)) {}
+  void* take(size_t bytes) {
+    void* r = p ? p + used : nullptr;
+    used += cnna_round_up(bytes, 256);
+    return r;
+  }
+};
+
+}  // namespace cnna_desc_util

@@ -86,3 +86,143 @@ int launch_aggregate(int dtype, const AggArgs& a, hipStream_t s);
 int launch_merge(int dtype, const AggArgs& a, hipStream_t s);
 // W0 (dout, din, K) -> W0p (dout, K*din) with W0p[o][r*din + c] = W0[o][c][r]
 int launch_permute_w0(int dtype, const void* w0, void* w0p, int dout, int din, int K, hipStream_t s);
+
+// ================================================================ backward
+// Gradient GEMM: out[m][n] = sum_k A[m][k] * W[n][k] with
+//   A: ROWS a[m * lda + k]  |  TRANS a[k * lda + m]
+//   W: ROWS w[n * ldw + k]  |  TRANS w[k * ldw + n], optionally three
+//      matrices stacked along k (w_krows rows each).
+// Without part: T into o (splits must be 1).  With part: fp32 partial sums
+// part[s][m][n] over k-chunks of kchunk, summed by launch_splitk_reduce.
+enum { GG_ROWS = 0, GG_TRANS = 1 };
+struct GradGemmArgs {
+  int M, Nc, Kd;
+  const void* a;
+  int64_t lda;
+  int amode;
+  const void* w[3];
+  int64_t ldw;
+  int wmode;
+  int w_krows;       // 0: single W; else rows of k per stacked pointer
+  void* o;
+  int64_t ldo;
+  float* part;
+  int splits, kchunk;
+  int avec, bvec;    // set by the launcher
+};
+// split count for a weight-gradient GEMM (shared by launcher and workspace sizing)
+inline int grad_gemm_splits(int M, int Nc, int Kd, int bk) {
+  const int tiles = ((M + 127) / 128) * ((Nc + 127) / 128);
+  int s = (512 + tiles - 1) / tiles;
+  const int maxs = (Kd + 8 * bk - 1) / (8 * bk);   // at least 8 k-tiles per split
+  if (s > maxs) s = maxs;
+  return s < 1 ? 1 : s;
+}
+inline int grad_gemm_bk(int dtype) { return dtype == 1 ? 64 : 32; }
+int launch_gemm_grad(int dtype, const GradGemmArgs& g, hipStream_t s);
+
+// Sum of split-K partials into up to three row blocks of T outputs, with an
+// optional column permutation n = r*pdin + c -> c*pK + r (conv weight layout).
+struct ReduceArgs {
+  const float* part;
+  int splits, M, Nc;
+  void* o[3];
+  int rows_each;
+  int64_t ldo;
+  int pdin, pK;      // pdin > 0: permute columns
+};
+int launch_splitk_reduce(int dtype, const ReduceArgs& r, hipStream_t s);
+
+// Inverse head merge: dy (BH, N, dk) token-major from dZ (B, N, C).
+int launch_unmerge(int dtype, const void* dz, void* dy, int BH, int N, int dk, int H, int C,
+                   hipStream_t s);
+
+// P[m][r*din + c] = w[m, r] * v[idx[m, r], c]  (materialised gathered input, standard conv)
+int launch_gather_p(int dtype, const void* v, const int32_t* idx, const float* w, void* P, int BH,
+                    int N, int K, int din, int dkp, hipStream_t s);
+
+// Per token: neighbour-weight gradient, softmax / weight backward, similarity
+// gradient coefficients and the key gradient; depthwise-weight partial sums.
+struct TokBwdArgs {
+  const void* g;        // depthwise modes: (BH, N, din) gradient at the depthwise-conv output
+  const void* dP;       // standard conv: (BH*N*K, din) gradient of the gathered input
+  const void* v;        // (BH, N, dkp)
+  const void* k;        // (BH, N, dkp), normalised for cosine
+  const void* q;        // (BH, Nq, dkp), normalised for cosine
+  const float* kn;      // squared key norms (cosine, euclidean)
+  const int32_t* idx;   // (BH, N, K)
+  const float* vals;    // (BH, N, K)
+  const float* w;       // (BH, N, K)
+  const int32_t* inv;   // sampled: token -> candidate column (or >= Nq)
+  const void* w0;       // depthwise weight (din, 1, K)
+  float* coef;          // out: (BH, N, K) similarity-gradient coefficient
+  float* w0part;        // out: (gridDim, din, K) depthwise-weight partials
+  void* dst;            // dK rows (B*N) of stride ldd, columns offd + h*dk + c
+  int64_t ldd;
+  int offd;
+  int BH, N, Nq, K, din, dk, dkp, H;
+  int metric, softmax, sampled, std_conv;
+  float scale;          // matmul: 1/sqrt(d_k)
+  int nblk;             // set by the launcher
+};
+int launch_tok_bwd(int dtype, const TokBwdArgs& a, hipStream_t s);
+// number of blocks of launch_tok_bwd (sizes the w0part buffer)
+inline int tok_bwd_blocks(int BH, int N) {
+  const long long w = ((long long)BH * N + 3) / 4;
+  return (int)(w < 2048 ? (w < 1 ? 1 : w) : 2048);
+}
+int launch_w0_reduce(int dtype, const float* part, int nblk, int n, void* out, hipStream_t s);
+
+// Deterministic reverse adjacency: entries e = i*K + r of each (b, h) bucketed
+// by key (CSR_TOKEN: idx[e]; CSR_COLUMN: inv[idx[e]] for sampled r >= 1 that
+// are not the masked self column), sorted by e inside each bucket.
+enum { CSR_TOKEN = 0, CSR_COLUMN = 1 };
+struct CsrArgs {
+  const int32_t* idx;
+  const int32_t* inv;
+  int mode;
+  int BH, N, K, nkeys;
+  int32_t* cnt;    // (BH, nkeys)
+  int32_t* off;    // (BH, nkeys + 1)
+  int32_t* tmp;    // (BH, N*K)
+  int32_t* list;   // (BH, N*K)
+};
+int launch_csr(const CsrArgs& c, hipStream_t s);
+// inv[t] = smallest column j with cand[j] == t, or Nq
+int launch_inv_map(const int32_t* cand, int Nq, int N, int32_t* inv, hipStream_t s);
+
+// Pull reductions over a CSR: dV (sum of w * dP over the entries that read a
+// value row) and dQ (sum of coef * k over the entries that selected a column).
+struct PullArgs {
+  const int32_t* off;
+  const int32_t* list;
+  int nkeys;
+  int do_v, do_q;
+  // dV
+  const void* g;       // depthwise modes: (BH, N, din)
+  const void* dP;      // standard: (BH*N*K, din)
+  const void* w0;      // depthwise weight (din, 1, K)
+  const float* w;      // (BH, N, K)
+  int std_conv;
+  void* dst_v;
+  int64_t ld_v;
+  int off_v;
+  // dQ
+  const float* coef;
+  const void* k;       // (BH, N, dkp)
+  const void* q;       // (BH, nkeys, dkp)
+  const float* qn;     // squared norms of q rows
+  int metric;
+  void* dst_q;
+  int64_t ld_q;
+  int off_q;
+  int BH, N, K, din, dk, dkp, H;
+};
+int launch_pull(int dtype, const PullArgs& p, hipStream_t s);
+
+// sampled rows: xs[b, j] = x[b, cand[j]];  dx[b, cand[j]] += dxs[b, j] in j order
+int launch_gather_rows(int dtype, const void* x, int64_t ldx, const int32_t* cand, void* xs, int B,
+                       int N, int Nq, int C, hipStream_t s);
+int launch_scatter_rows(int dtype, const void* dxs, const int32_t* cand, void* dx, int B, int N,
+                        int Nq, int C, hipStream_t s);
+int launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t s);

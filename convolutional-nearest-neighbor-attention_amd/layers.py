@@ -118,7 +118,8 @@ class MultiHeadConvNNAttention(nn.Module):
                           self.magnitude_type, self.convolution_type, self.softmax_topk_val,
                           cand is not None, self.coordinate_encoding)
         w0, w1 = self._conv_weights()
-        z = ops.ConvNNCore.apply(x, self.W_q.weight, self.W_k.weight, self.W_v.weight, w0, w1, cand, d)
+        z = ops.ConvNNCore.apply(x, self.W_q.weight, self.W_k.weight, self.W_v.weight, w0, w1, cand, d,
+                                 True)
         # dropout on the conv output (layers.py:316); elementwise, so applying it
         # after the head merge is the same operation on permuted elements
         z = self.dropout(z)

@@ -83,7 +83,9 @@ int cnna_head_stride(const cnna_desc* d);
  *   cand (Nq) int32 sampled token indices, NULL for 'all'
  *   W*   (C, C) nn.Linear weights [out, in]
  *   q    (B*H, Nq, dkp); k, v (B*H, N, dkp)
- *   qn, kn  fp32 squared norms (B*H*Nq), (B*H*N): euclidean only, else NULL */
+ *   qn, kn  fp32 squared norms (B*H*Nq), (B*H*N) of the rows before
+ *           normalisation: required for euclidean, optional for cosine (the
+ *           backward needs them), else NULL */
 int cnna_project_qkv(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* cand,
                      const void* Wq, const void* Wk, const void* Wv,
                      void* q, void* k, void* v, float* qn, float* kn, void* stream);
@@ -125,6 +127,58 @@ int cnna_forward(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* 
                  const void* Wq, const void* Wk, const void* Wv, const void* Wo,
                  const void* conv_w0, const void* conv_w1, void* out, int64_t ldo,
                  void* ws, size_t ws_bytes, void* stream);
+
+/* ------------------------------------------------------------ backward
+ * Autograd of the stages above (what loss.backward() computes through
+ * layers.py:261-450).  The reference differentiates the dense (B*H, N, Nq)
+ * similarity matrix; these entry points only touch the K selected entries
+ * of each row.  All sums run in a fixed order: results are deterministic. */
+
+/* Tensors saved by the forward stages (outputs of cnna_project_qkv and
+ * cnna_select). qn/kn are required for cosine and euclidean. */
+typedef struct cnna_saved {
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* qn;
+  const float* kn;
+  const int32_t* idx;
+  const float* vals;
+  const float* w;
+} cnna_saved;
+
+/* Gradients written by cnna_core_backward, dtype of the descriptor.
+ *   dx (B, N, C) contiguous; dWq, dWk, dWv (C, C); dconv_w0 / dconv_w1 shaped
+ *   like conv_w0 / conv_w1 (dconv_w1 only for depthwise-separable). */
+typedef struct cnna_grads {
+  void* dx;
+  void* dWq;
+  void* dWk;
+  void* dWv;
+  void* dconv_w0;
+  void* dconv_w1;
+} cnna_grads;
+
+/* Backward of cnna_output_proj (nn.Linear W_o, layers.py:320):
+ *   dz = dout @ Wo,  dWo = dout^T @ z.   dout (B, N, C) row stride ld_dout;
+ *   z, dz (B, N, C) contiguous; dWo (C, C). */
+size_t cnna_output_proj_backward_workspace(const cnna_desc* d);
+int cnna_output_proj_backward(const cnna_desc* d, const void* z, const void* Wo, const void* dout,
+                              int64_t ld_dout, void* dz, void* dWo, void* ws, size_t ws_bytes,
+                              void* stream);
+
+/* Backward of cnna_project_qkv + cnna_select + cnna_aggregate: from dz, the
+ * gradient at the input of W_o (B, N, C contiguous), to x, W_q, W_k, W_v and
+ * the conv weights.  Covers the head merge (layers.py:247-259, 316-317), the
+ * conv (layers.py:313), the weights of _prime/_prime_softmax/_prime_N/
+ * _prime_softmax_N (layers.py:342-437, softmax backward and the self-slot /
+ * self-mask constants), the similarity (layers.py:323-340) and the projections
+ * (layers.py:264-265, 274, 286, 299). */
+size_t cnna_core_backward_workspace(const cnna_desc* d);
+int cnna_core_backward(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* cand,
+                       const void* Wq, const void* Wk, const void* Wv, const void* conv_w0,
+                       const void* conv_w1, const cnna_saved* saved, const void* dz,
+                       const cnna_grads* grads, void* ws, size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -277,23 +277,28 @@ def mask_self(S: torch.Tensor, cand: torch.Tensor, cfg: Config) -> torch.Tensor:
 # neighbour selection and weights (layers.py:342-437)
 # --------------------------------------------------------------------------
 
-def select_neighbours(S: torch.Tensor, cfg: Config, cand: Optional[torch.Tensor]):
+def select_neighbours(S: torch.Tensor, cfg: Config, cand: Optional[torch.Tensor],
+                      cols: Optional[torch.Tensor] = None):
     """Returns (idx (BH,N,K) int64 token indices, vals (BH,N,K) logits/values).
 
     all:     top-K of S along candidates (layers.py:344, 391).
     sampled: top-(K-1) over Ns candidates, mapped through ``cand``, with the
              token itself prepended at rank 0 with value 1.0
              (layers.py:363-376, 410-423).  ``K - 1`` candidates must exist.
+    ``cols`` (BH, N, K or K-1) replaces the top-k search by a given choice of
+    candidate columns (test hook: gradients on a fixed selection).
     """
     BH, N, Nq = S.shape
-    if cand is None:
-        if cfg.K > Nq:
-            raise RuntimeError("selected index k out of range")
-        vals, idx = stable_topk(S, cfg.K, cfg.maximum)
-        return idx, vals
-    if cfg.K - 1 > Nq:
+    ksel = cfg.K if cand is None else cfg.K - 1
+    if ksel > Nq:
         raise RuntimeError("selected index k out of range")
-    vals, tk = stable_topk(S, cfg.K - 1, cfg.maximum)
+    if cols is not None:
+        tk = cols.to(torch.int64)
+        vals = torch.gather(S, -1, tk)
+    else:
+        vals, tk = stable_topk(S, ksel, cfg.maximum)
+    if cand is None:
+        return tk, vals
     mapped = cand[tk]
     self_idx = torch.arange(N).view(1, N, 1).expand(BH, N, 1)
     idx = torch.cat([self_idx, mapped], dim=-1)
@@ -365,12 +370,14 @@ class Intermediates:
 
 
 def forward(x: torch.Tensor, p: Params, cfg: Config, cand: Optional[torch.Tensor] = None,
-            mode: str = "reference", generator=None, return_intermediates: bool = False):
+            mode: str = "reference", generator=None, return_intermediates: bool = False,
+            cols: Optional[torch.Tensor] = None):
     """Restatement of ``MultiHeadConvNNAttention.forward`` (layers.py:261-321).
 
     ``cand`` injects the sampled candidate indices; when None they are drawn
     with ``sample_indices`` (randperm on ``generator``).  Dropout is the
-    identity (eval mode).
+    identity (eval mode).  ``cols`` fixes the selected candidate columns (see
+    ``select_neighbours``); the function stays differentiable in x and p.
     """
     if mode not in ("reference", "exact"):
         raise ValueError(mode)
@@ -404,7 +411,7 @@ def forward(x: torch.Tensor, p: Params, cfg: Config, cand: Optional[torch.Tensor
         S = mask_self(S, cand, cfg)
 
     # 3. neighbours, weights, gather, conv
-    idx, vals = select_neighbours(S, cfg, cand)
+    idx, vals = select_neighbours(S, cfg, cand, cols)
     vv = v.to(wk)
     if mode == "reference" and not cfg.softmax_topk_val and not cfg.maximum:
         # literal division, layers.py:352-353 / 382-383

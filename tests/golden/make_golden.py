@@ -17,7 +17,9 @@ operator whose composition only the reference itself can pin:
 
 Each case is written as ``<name>.npz`` holding only data: the input ``x``,
 the module's parameters (by their reference names), the sampled candidate
-indices (when any), the output, and the constructor arguments as JSON.
+indices (when any), the output, the constructor arguments as JSON, and the
+reference's autograd gradients for an upstream gradient ``dout``:
+``grad:x`` and ``grad:<parameter name>``.
 Cases run in float64 (tight comparison) and float32.
 """
 from __future__ import annotations
@@ -90,10 +92,17 @@ def main(ref_root: str) -> None:
                     if name_p.startswith("conv"):
                         p.copy_(torch.randn_like(p))
             x = torch.randn(B, N, kw["d_hidden"], dtype=dtype)
+            dout = torch.randn(B, N, kw["d_hidden"], dtype=dtype)
             fwd_seed = 7 + i
             torch.manual_seed(fwd_seed)
-            with torch.no_grad():
-                out = mod(x)
+            xr = x.clone().requires_grad_(True)
+            out = mod(xr)
+            grad_error = None
+            try:
+                out.backward(dout)
+            except RuntimeError as e:   # the reference's own autograd failure
+                grad_error = str(e).split("\n")[0]
+            out = out.detach()
             cand = None
             if kw["sampling_type"] == "random":
                 torch.manual_seed(fwd_seed)
@@ -101,9 +110,15 @@ def main(ref_root: str) -> None:
             elif kw["sampling_type"] == "spatial":
                 pad = kw["sample_padding"]
                 cand = torch.linspace(pad, N - pad - 1, kw["num_samples"]).long()
-            arrays = {"x": x.numpy(), "out": out.numpy()}
+            arrays = {"x": x.numpy(), "out": out.numpy(), "dout": dout.numpy()}
             for name_p, p in mod.state_dict().items():
                 arrays["param:" + name_p] = p.numpy()
+            if grad_error is None:
+                arrays["grad:x"] = xr.grad.numpy()
+                for name_p, p in mod.named_parameters():
+                    arrays["grad:" + name_p] = p.grad.numpy()
+            else:
+                arrays["grad_error"] = np.frombuffer(grad_error.encode(), dtype=np.uint8)
             if cand is not None:
                 arrays["cand"] = cand.numpy()
             arrays["ctor"] = np.frombuffer(json.dumps(kw).encode(), dtype=np.uint8)

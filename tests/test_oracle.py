@@ -177,6 +177,56 @@ def test_spatial_indices_are_1d_linspace():
     assert O.sample_indices(cfg, 197).tolist() == [0, 28, 56, 84, 112, 140, 168, 196]
 
 
+@pytest.mark.parametrize("path", GOLDEN, ids=[os.path.basename(p) for p in GOLDEN])
+def test_oracle_grads_match_reference_golden(path):
+    """Backward: torch autograd through the oracle equals the reference's own
+    autograd (fixtures hold grad:x and grad:<param> for an upstream dout)."""
+    z = np.load(path, allow_pickle=False)
+    if "grad_error" in z.files:
+        # the reference cannot differentiate sampled euclidean (in-place self
+        # mask on the output of sqrt, layers.py:278-305); nothing to pin
+        assert "modified by an inplace operation" in bytes(z["grad_error"]).decode()
+        return
+    cfg, p, x, cand, _ = load_case(path)
+    dout = torch.from_numpy(z["dout"])
+    names = ["W_q", "W_k", "W_v", "W_o", "conv0", "conv1"]
+    ts = [None if t is None else t.clone().requires_grad_(True)
+          for t in (x, p.W_q, p.W_k, p.W_v, p.W_o, p.conv0, p.conv1)]
+    out = O.forward(ts[0], O.Params(*ts[1:]), cfg, cand=cand, mode="reference")
+    out.backward(dout)
+    ref_names = {"W_q": "W_q.weight", "W_k": "W_k.weight", "W_v": "W_v.weight",
+                 "W_o": "W_o.weight"}
+    if cfg.convolution_type == "depthwise-separable":
+        ref_names.update(conv0="conv.0.weight", conv1="conv.1.weight")
+    else:
+        ref_names.update(conv0="conv.weight")
+    tol = dict(rtol=1e-9, atol=1e-10) if x.dtype == torch.float64 else dict(rtol=2e-4, atol=2e-5)
+    torch.testing.assert_close(ts[0].grad, torch.from_numpy(z["grad:x"]), **tol)
+    for n, t in zip(names, ts[1:]):
+        if t is None:
+            continue
+        torch.testing.assert_close(t.grad, torch.from_numpy(z["grad:" + ref_names[n]]), **tol,
+                                   msg=lambda m: f"{n}: {m}")
+
+
+def test_oracle_cols_hook_reproduces_topk():
+    """Passing the top-k's own columns back as ``cols`` changes nothing."""
+    for sampling in ("all", "random"):
+        cfg = O.Config(d_hidden=12, num_heads=3, K=4, sampling_type=sampling, num_samples=7,
+                       seq_length=15, magnitude_type="cosine")
+        p = O.init_params(cfg, seed=3, dtype=torch.float64)
+        x = torch.randn(2, 15, 12, dtype=torch.float64)
+        cand = O.sample_indices(cfg, 15, generator=torch.Generator().manual_seed(1))
+        out, it = O.forward(x, p, cfg, cand=cand, mode="exact", return_intermediates=True)
+        if cand is None:
+            cols = it.idx
+        else:
+            inv = {int(t): j for j, t in enumerate(cand.tolist())}
+            cols = torch.tensor([[[inv[int(t)] for t in row[1:]] for row in bh] for bh in it.idx])
+        out2 = O.forward(x, p, cfg, cand=cand, mode="exact", cols=cols)
+        assert torch.equal(out, out2)
+
+
 def test_gradcheck_oracle_f64():
     B, N, C, H = 1, 6, 4, 2
     cfg = O.Config(d_hidden=C, num_heads=H, K=3, seq_length=N, convolution_type="standard")
