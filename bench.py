@@ -5,10 +5,14 @@
 One step = one forward of ``MultiHeadConvNNAttention`` (eval mode) over one
 batch of synthetic input already resident in HBM.  The default workload is
 B=32, N=1024, C=384, H=3, K=9, bf16, matmul similarity,
-depthwise conv, sampling 'all'.  Prints one JSON line with tokens/s, the
-roofline of the dominant kernel (timed with HIP events on the launch stream)
-and the CPU baseline (the oracle's restatement of the reference op sequence
-on a bounded sample, timed on this host's cores).
+depthwise conv, sampling 'all'.  ``--config c5`` times a training step
+instead: forward + backward (loss gradient dout fixed, all parameter and
+input gradients) at B=8, N=4096, C=768, H=3, K=16, standard conv.
+
+Prints one JSON line with tokens/s, the roofline of the dominant forward
+kernel (timed with HIP events on the launch stream) and the CPU baseline (the
+oracle's restatement of the reference op sequence on a bounded sample, timed
+on this host's cores).
 """
 from __future__ import annotations
 
@@ -36,7 +40,9 @@ CONFIGS = {
     "c1": (64, 65, 192, 3, 9, torch.float32, "cosine", "depthwise", "all", -1, 0),
     "c4a": (128, 197, 192, 3, 9, torch.float32, "matmul", "depthwise", "random", 64, 2),
     "c4b": (128, 197, 192, 3, 9, torch.float32, "matmul", "depthwise", "spatial", 8, 2),
+    "c5": (8, 4096, 768, 3, 16, torch.bfloat16, "matmul", "standard", "all", -1, 3),
 }
+TRAIN = {"c5"}
 
 
 def parse():
@@ -69,23 +75,36 @@ def main():
     from layers import MultiHeadConvNNAttention
 
     B, N, C, H, K, dtype, metric, conv, sampling, ns, seed = CONFIGS[args.config]
+    train = args.config in TRAIN
     dev = "cuda"
     torch.manual_seed(seed)
     m = MultiHeadConvNNAttention(C, H, 0.0, K, sampling, ns, 0, metric, seq_length=N,
-                                 convolution_type=conv).to(dev).to(dtype).eval()
+                                 convolution_type=conv).to(dev).to(dtype)
+    m.train(train)
     x = torch.randn(B, N, C, device=dev).to(dtype)
     Nq = N if sampling == "all" else ns
 
     # ---- whole-layer timing
-    with torch.no_grad():
-        for _ in range(args.warmup):
-            m(x)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            m(x)
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
+    if train:
+        xg = x.clone().requires_grad_(True)
+        dout = torch.randn(B, N, C, device=dev).to(dtype)
+
+        def step():
+            m.zero_grad(set_to_none=True)
+            xg.grad = None
+            m(xg).backward(dout)
+    else:
+        def step():
+            with torch.no_grad():
+                m(x)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
     ms = (t1 - t0) * 1e3 / args.steps
     tokens = B * N
     value = tokens / (ms / 1e3)
@@ -138,6 +157,10 @@ def main():
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None}
 
     total_flops = proj_f + sim_f + conv_f
+    if train:
+        # backward: twice the projection and conv GEMM work plus the sparse
+        # similarity / softmax / gather terms over the K selected entries
+        total_flops += 2 * (proj_f + conv_f) + 8 * B * N * K * C
     layer_tflops = total_flops / (ms / 1e3) / 1e12
 
     # ---- CPU baseline: the oracle's reference-mode op sequence on a bounded sample
@@ -146,7 +169,7 @@ def main():
         from oracle import cnna_oracle as O
         ncores = len(os.sched_getaffinity(0))
         torch.set_num_threads(ncores)
-        bs = max(1, min(args.cpu_sample_batch, B))
+        bs = 1 if train else max(1, min(args.cpu_sample_batch, B))
         cfg = O.Config(d_hidden=C, num_heads=H, K=K, sampling_type=sampling, num_samples=ns,
                        magnitude_type=metric, seq_length=N, convolution_type=conv)
         p = O.Params.from_module_state({k_: v_.detach().cpu() for k_, v_ in m.state_dict().items()}, conv)
@@ -158,26 +181,40 @@ def main():
             cdt = torch.float32
         xc, p = xc.to(cdt), p.to(dtype=cdt)
         cc = None if cand is None else cand.cpu().long()
-        O.forward(xc, p, cfg, cand=cc, mode="reference")          # warm-up
+
+        def cpu_step():
+            if not train:
+                with torch.no_grad():
+                    O.forward(xc, p, cfg, cand=cc, mode="reference")
+                return
+            ts = [t.clone().requires_grad_(True) for t in (xc, p.W_q, p.W_k, p.W_v, p.W_o, p.conv0)]
+            out = O.forward(ts[0], O.Params(*ts[1:], p.conv1), cfg, cand=cc, mode="reference")
+            out.backward(torch.ones_like(out))
+
+        cpu_step()                                                 # warm-up
         reps, t_cpu = 0, 0.0
         while reps < 3 or (t_cpu < 10.0 and reps < 20):
             c0 = time.perf_counter()
-            O.forward(xc, p, cfg, cand=cc, mode="reference")
+            cpu_step()
             t_cpu += time.perf_counter() - c0
             reps += 1
         cpu = {"value": round(bs * N * reps / t_cpu, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
                "kind": "port",
-               "sample": f"{reps} forwards of {bs} of {B} sequences (N={N}) in "
+               "sample": f"{reps} {'training steps' if train else 'forwards'} of {bs} of {B} sequences (N={N}) in "
                          f"{str(cdt).replace('torch.', '')}, oracle reference-mode op sequence",
                "affinity_cores": ncores, "os_cpu_count": os.cpu_count(), "torch": torch.__version__}
 
+    metric_name = "ConvNN-Attn layer tokens/s (N=1024,C=384,K=9,bf16); % MFMA/HBM roofline"
+    if train:
+        metric_name = "ConvNN-Attn training-step tokens/s (N=4096,C=768,K=16,standard conv,bf16)"
     rec = {
-        "metric": "ConvNN-Attn layer tokens/s (N=1024,C=384,K=9,bf16); % MFMA/HBM roofline",
+        "metric": metric_name,
         "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if dtype == torch.bfloat16 else "f32",
         "data": "synthetic: x ~ N(0,1), random-init weights (seeded)",
-        "config": {"workload": f"{args.config}: MultiHeadConvNNAttention forward B={B} N={N} C={C} "
+        "config": {"workload": f"{args.config}: MultiHeadConvNNAttention "
+                               f"{'forward+backward' if train else 'forward'} B={B} N={N} C={C} "
                                f"H={H} K={K} {metric} {conv} sampling={sampling}",
                    "B": B, "N": N, "C": C, "H": H, "K": K, "sampling": sampling},
         "roofline": roof,

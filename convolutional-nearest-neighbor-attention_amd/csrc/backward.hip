@@ -107,22 +107,6 @@ __global__ __launch_bounds__(256) void unmerge_kernel(const T* dz, T* dy, int BH
   dy[e] = dz[src];
 }
 
-// ------------------------------------------------------------------ gather P
-template <typename T>
-__global__ __launch_bounds__(256) void gather_p_kernel(const T* v, const int32_t* idx,
-                                                       const float* w, T* P, int BH, int N, int K,
-                                                       int din, int dkp) {
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;   // over BH*N*K*din
-  const int64_t tot = (int64_t)BH * N * K * din;
-  if (e >= tot) return;
-  const int64_t ent = e / din;              // (bh*N + i)*K + r
-  const int c = (int)(e - ent * din);
-  const int64_t tok = ent / K;
-  const int bh = (int)(tok / N);
-  const int j = idx[ent];
-  stf(P + e, w[ent] * ldf(v + ((int64_t)bh * N + j) * dkp + c));
-}
-
 // ------------------------------------------------------------------ tok_bwd
 template <typename T, int CPL, int KMAX, bool DW>
 __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
@@ -572,23 +556,6 @@ int launch_unmerge(int dtype, const void* dz, void* dy, int BH, int N, int dk, i
   else if (dtype == CNNA_F32)
     hipLaunchKernelGGL(unmerge_kernel<float>, grid_for(n), dim3(256), 0, s,
                        static_cast<const float*>(dz), static_cast<float*>(dy), BH, N, dk, H, C);
-  else
-    return CNNA_ERR_DTYPE;
-  return (int)hipGetLastError();
-}
-
-int launch_gather_p(int dtype, const void* v, const int32_t* idx, const float* w, void* P, int BH,
-                    int N, int K, int din, int dkp, hipStream_t s) {
-  const int64_t n = (int64_t)BH * N * K * din;
-  if (n <= 0) return 0;
-  if (dtype == CNNA_BF16)
-    hipLaunchKernelGGL(gather_p_kernel<uint16_t>, grid_for(n), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(v), idx, w, static_cast<uint16_t*>(P), BH, N, K,
-                       din, dkp);
-  else if (dtype == CNNA_F32)
-    hipLaunchKernelGGL(gather_p_kernel<float>, grid_for(n), dim3(256), 0, s,
-                       static_cast<const float*>(v), idx, w, static_cast<float*>(P), BH, N, K, din,
-                       dkp);
   else
     return CNNA_ERR_DTYPE;
   return (int)hipGetLastError();

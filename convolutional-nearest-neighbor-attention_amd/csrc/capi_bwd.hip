@@ -15,7 +15,7 @@ using namespace cnna_desc_util;
 namespace {
 
 struct CorePlan {
-  void *dy, *t1, *dt1, *w0p, *P, *dP, *dqkv, *dqs, *xs, *dxs;
+  void *dy, *t1, *dt1, *w0p, *dP, *dqkv, *dqs, *xs, *dxs;
   float *coef, *w0part, *part;
   int32_t *cnt, *off, *tmp, *list, *cnt2, *off2, *tmp2, *list2, *inv;
   size_t bytes;
@@ -40,7 +40,6 @@ CorePlan plan_core(const cnna_desc* d, void* ws) {
   }
   if (d->conv == CNNA_CONV_STANDARD) {
     p.w0p = c.take(dk * K * din * es);
-    p.P = c.take(ent * din * es);
     p.dP = c.take(ent * din * es);
   }
   p.coef = static_cast<float*>(c.take(ent * 4));
@@ -187,14 +186,15 @@ int cnna_core_backward(const cnna_desc* d, const void* x, int64_t ldx, const int
       return st;
     g_dw = p.dt1;
   } else {
-    // standard: dP = dy @ W0p ; dW0p = dy^T P (P gathered), permuted back to (dk, din, K)
+    // standard: dP = dy @ W0p ; dW0p = dy^T P with P[tok][r*din + c] = w * v[idx] gathered
+    // inside the GEMM, permuted back to (dk, din, K)
     if ((st = launch_permute_w0(dt, conv_w0, p.w0p, dk, din, K, s))) return st;
     GradGemmArgs g = gg(ntok, K * din, dk, p.dy, dk, GG_ROWS, p.w0p, (int64_t)K * din, GG_TRANS);
     g.o = p.dP;
     g.ldo = (int64_t)K * din;
     if ((st = launch_gemm_grad(dt, g, s))) return st;
-    if ((st = launch_gather_p(dt, sv->v, sv->idx, sv->w, p.P, BH, N, K, din, dkp, s))) return st;
-    g = gg(dk, K * din, ntok, p.dy, dk, GG_TRANS, p.P, (int64_t)K * din, GG_TRANS);
+    g = gg(dk, K * din, ntok, p.dy, dk, GG_TRANS, sv->v, 0, GG_GATHER_T);
+    g.g_idx = sv->idx; g.g_w = sv->w; g.g_K = K; g.g_N = N; g.g_din = din; g.g_dkp = dkp;
     if ((st = weight_grad(dt, g, p.part, gr->dconv_w0, nullptr, nullptr, dk, (int64_t)din * K, din,
                           K, s)))
       return st;

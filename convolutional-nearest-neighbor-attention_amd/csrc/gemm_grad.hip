@@ -1,13 +1,22 @@
 // MFMA GEMM for the backward pass: out[m][n] = sum_k A[m][k] * W[n][k] with
-// either operand row-major or transposed.  Transposed operands are read along
-// their contiguous index and transposed while being staged into LDS.  Covers
-// the gradients of the projections (nn.Linear at layers.py:264-265, 274, 320)
-// and of the standard / pointwise convolutions (layers.py:187-228).
+// either operand row-major (ROWS) or transposed (TRANS: k is the slow index),
+// and a gathered transposed W (GATHER_T: the standard conv's input P, built
+// from the neighbour lists on the fly).  Covers the gradients of the
+// projections (nn.Linear at layers.py:264-265, 274, 320) and of the standard /
+// pointwise convolutions (layers.py:187-228).
 //
-// Tiling as in the forward GEMM: 128 x 128 x BK tiles, four waves of 64 x 64,
-// fp32 accumulation, register prefetch of the next k-tile.  Weight gradients
-// reduce over B*N rows: they split k into chunks written as fp32 partials and
-// summed in a fixed order by splitk_reduce, so results are deterministic.
+// Tiling: 128 x 128 output tiles, BK = 128 bytes of k per step, four waves of
+// 64 x 64, fp32 accumulation, register prefetch of the next k-step.
+//
+// LDS holds each operand tile as 128 rows x 8 chunks of 16 bytes (k
+// contiguous inside a chunk), chunk index XOR-swizzled by the row so that both
+// the staging writes and the MFMA fragment reads spread over the banks.
+//   ROWS   a thread loads 16-byte vectors along k and writes them as chunks;
+//   TRANS  a thread loads 4 consecutive k of one 16-byte row-vector each,
+//          transposes the 4 x RV block in registers and writes RV pieces of
+//          4 consecutive k (8 or 16 bytes): no scalar LDS writes.
+// Weight gradients reduce over B*N rows: they split k into chunks written as
+// fp32 partials and summed in a fixed order by splitk_reduce (deterministic).
 #include "common.h"
 #include "kernels.h"
 
@@ -15,54 +24,57 @@ namespace {
 
 constexpr int BM = 128, BN = 128;
 
-template <typename T> struct GCfg;
-template <> struct GCfg<uint16_t> { static constexpr int BK = 64, VEC = 8; };
-template <> struct GCfg<float> { static constexpr int BK = 32, VEC = 4; };
-
-template <typename T, int VEC>
-union GPack {
-  u32x4_t u;
-  T e[VEC];
+template <typename T> struct GCfg {
+  static constexpr int CE = 16 / sizeof(T);   // elements per 16-byte chunk
+  static constexpr int BK = 8 * CE;           // k per step (one 128-byte row)
+  static constexpr int RV = CE;               // rows per TRANS vector
+  static constexpr int RB = 128 / RV;         // TRANS row-vectors per tile
 };
 
-// One operand tile (128 rows of the output dimension x BK of k) per k-step.
-// ROWS: thread slot -> (row, k-vector), 16-byte loads along k.
-// TRANS: thread slot -> (k, row-vector), 16-byte loads along the rows.
+CNNA_DEV int swz(int row) { return (row ^ (row >> 3)) & 7; }
+
+// element offset of (row, k) in a swizzled tile
+template <typename T>
+CNNA_DEV int lds_off(int row, int k) {
+  constexpr int CE = GCfg<T>::CE;
+  return row * (8 * CE) + (((k / CE) ^ swz(row)) * CE) + (k % CE);
+}
+
+template <typename T>
+union GPack {
+  u32x4_t u;
+  T e[GCfg<T>::CE];
+};
+
+struct GatherArgs {
+  const int32_t* idx;
+  const float* w;
+  int K, N, din, dkp;
+};
+
 template <typename T, int MODE>
 struct Operand {
-  static constexpr int BK = GCfg<T>::BK, VEC = GCfg<T>::VEC;
-  static constexpr int NV = BM * (BK / VEC) / 256;
-  static constexpr int LDS_STRIDE = BK + VEC;
+  static constexpr int CE = GCfg<T>::CE, RV = GCfg<T>::RV, RB = GCfg<T>::RB;
+  static constexpr int NV = 4;   // 16-byte vectors per thread per tile (both layouts)
 
-  static CNNA_DEV void slot(int tid, int i, int& x, int& y) {
-    const int e = tid + i * 256;
-    if (MODE == GG_ROWS) {
-      x = e / (BK / VEC);              // row
-      y = (e % (BK / VEC)) * VEC;      // k
-    } else {
-      x = e / (BM / VEC);              // k
-      y = (e % (BM / VEC)) * VEC;      // row
-    }
-  }
-
-  // rows [r0, r0 + 128) of a (nrows x Kd) operand, k in [k0, k0 + BK) below kend
-  static CNNA_DEV void fetch(GPack<T, VEC> (&reg)[NV], const T* const (&base)[3], int krows,
-                             int64_t ld, bool vec, int nrows, int r0, int k0, int kend, int tid) {
+  // rows [r0, r0 + 128) of the operand, k in [k0, k0 + BK) below kend
+  static CNNA_DEV void fetch(GPack<T> (&reg)[NV], const T* const (&base)[3], int krows, int64_t ld,
+                             bool vec, int nrows, int r0, int k0, int kend, int tid,
+                             const GatherArgs& ga) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      int x, y;
-      slot(tid, i, x, y);
       if (MODE == GG_ROWS) {
-        const int r = r0 + x, k = k0 + y;
+        const int e = tid + i * 256;
+        const int r = r0 + (e >> 3), k = k0 + (e & 7) * CE;
         const T* p = base[0] + (int64_t)r * ld + k;
-        if (r < nrows && vec && k + VEC <= kend) {
+        if (r < nrows && vec && k + CE <= kend) {
           reg[i].u = *reinterpret_cast<const u32x4_t*>(p);
         } else {
 #pragma unroll
-          for (int t = 0; t < VEC; ++t) reg[i].e[t] = (r < nrows && k + t < kend) ? p[t] : T(0);
+          for (int t = 0; t < CE; ++t) reg[i].e[t] = (r < nrows && k + t < kend) ? p[t] : T(0);
         }
-      } else {
-        const int k = k0 + x, r = r0 + y;
+      } else if (MODE == GG_TRANS) {
+        const int r = r0 + (tid % RB) * RV, k = k0 + (tid / RB) * 4 + i;
         int kb = 0, kr = k;
         if (krows > 0) {
           kb = k / krows;
@@ -70,26 +82,65 @@ struct Operand {
           kb = kb > 2 ? 2 : kb;
         }
         const T* p = base[kb] + (int64_t)kr * ld + r;
-        if (k < kend && vec && r + VEC <= nrows) {
+        if (k < kend && vec && r + RV <= nrows) {
           reg[i].u = *reinterpret_cast<const u32x4_t*>(p);
         } else {
 #pragma unroll
-          for (int t = 0; t < VEC; ++t) reg[i].e[t] = (k < kend && r + t < nrows) ? p[t] : T(0);
+          for (int t = 0; t < RV; ++t) reg[i].e[t] = (k < kend && r + t < nrows) ? p[t] : T(0);
+        }
+      } else {
+        // GATHER_T: rows n = r*din + c .. + RV of token k
+        const int n = r0 + (tid % RB) * RV, k = k0 + (tid / RB) * 4 + i;
+        if (k < kend && vec && n + RV <= nrows) {
+          const int rr = n / ga.din, c = n - rr * ga.din;
+          const int j = ga.idx[(int64_t)k * ga.K + rr];
+          const float wv = ga.w[(int64_t)k * ga.K + rr];
+          const T* p = base[0] + ((int64_t)(k - k % ga.N) + j) * ga.dkp + c;
+          GPack<T> v;
+          v.u = *reinterpret_cast<const u32x4_t*>(p);
+#pragma unroll
+          for (int t = 0; t < RV; ++t) stf(&reg[i].e[t], wv * ldf(&v.e[t]));
+        } else {
+#pragma unroll
+          for (int t = 0; t < RV; ++t) {
+            float x = 0.0f;
+            if (k < kend && n + t < nrows) {
+              const int rr = (n + t) / ga.din, c = (n + t) - rr * ga.din;
+              const int j = ga.idx[(int64_t)k * ga.K + rr];
+              x = ga.w[(int64_t)k * ga.K + rr] *
+                  ldf(base[0] + ((int64_t)(k - k % ga.N) + j) * ga.dkp + c);
+            }
+            stf(&reg[i].e[t], x);
+          }
         }
       }
     }
   }
 
-  static CNNA_DEV void stash(const GPack<T, VEC> (&reg)[NV], T* S, int tid) {
+  static CNNA_DEV void stash(const GPack<T> (&reg)[NV], T* S, int tid) {
+    if (MODE == GG_ROWS) {
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      int x, y;
-      slot(tid, i, x, y);
-      if (MODE == GG_ROWS) {
-        *reinterpret_cast<u32x4_t*>(&S[x * LDS_STRIDE + y]) = reg[i].u;
-      } else {
+      for (int i = 0; i < NV; ++i) {
+        const int e = tid + i * 256;
+        *reinterpret_cast<u32x4_t*>(&S[lds_off<T>(e >> 3, (e & 7) * CE)]) = reg[i].u;
+      }
+    } else {
+      // reg[i] = RV consecutive rows at k = kb*4 + i; write row j's 4 k values
+      const int rb = tid % RB, kb = tid / RB;
 #pragma unroll
-        for (int t = 0; t < VEC; ++t) S[(y + t) * LDS_STRIDE + x] = reg[i].e[t];
+      for (int j = 0; j < RV; ++j) {
+        T* dst = &S[lds_off<T>(rb * RV + j, kb * 4)];
+        if constexpr (sizeof(T) == 2) {
+          uint2 u;
+          u.x = (uint32_t)reg[0].e[j] | ((uint32_t)reg[1].e[j] << 16);
+          u.y = (uint32_t)reg[2].e[j] | ((uint32_t)reg[3].e[j] << 16);
+          *reinterpret_cast<uint2*>(dst) = u;
+        } else {
+          u32x4_t u;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) u[i] = __builtin_bit_cast(uint32_t, reg[i].e[j]);
+          *reinterpret_cast<u32x4_t*>(dst) = u;
+        }
       }
     }
   }
@@ -100,10 +151,9 @@ __global__ __launch_bounds__(256) void gemm_grad_kernel(GradGemmArgs g) {
   using M_ = Mfma<T>;
   using OA = Operand<T, AM>;
   using OW = Operand<T, WM>;
-  constexpr int BK = GCfg<T>::BK, VEC = GCfg<T>::VEC;
-  constexpr int LDS_STRIDE = BK + VEC;
-  __shared__ __attribute__((aligned(16))) T As[BM * LDS_STRIDE];
-  __shared__ __attribute__((aligned(16))) T Bs[BN * LDS_STRIDE];
+  constexpr int BK = GCfg<T>::BK;
+  __shared__ __attribute__((aligned(16))) T As[BM * BK];
+  __shared__ __attribute__((aligned(16))) T Bs[BN * BK];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -119,8 +169,10 @@ __global__ __launch_bounds__(256) void gemm_grad_kernel(GradGemmArgs g) {
   const T* const abase[3] = {static_cast<const T*>(g.a), nullptr, nullptr};
   const T* const wbase[3] = {static_cast<const T*>(g.w[0]), static_cast<const T*>(g.w[1]),
                              static_cast<const T*>(g.w[2])};
+  GatherArgs ga;
+  ga.idx = g.g_idx; ga.w = g.g_w; ga.K = g.g_K; ga.N = g.g_N; ga.din = g.g_din; ga.dkp = g.g_dkp;
 
-  GPack<T, VEC> ra[OA::NV], rw[OW::NV];
+  GPack<T> ra[OA::NV], rw[OW::NV];
   f32x16_t acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -130,16 +182,16 @@ __global__ __launch_bounds__(256) void gemm_grad_kernel(GradGemmArgs g) {
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
   if (kbeg < kend) {
-    OA::fetch(ra, abase, 0, g.lda, g.avec, g.M, m0, kbeg, kend, tid);
-    OW::fetch(rw, wbase, g.w_krows, g.ldw, g.bvec, g.Nc, n0, kbeg, kend, tid);
+    OA::fetch(ra, abase, 0, g.lda, g.avec, g.M, m0, kbeg, kend, tid, ga);
+    OW::fetch(rw, wbase, g.w_krows, g.ldw, g.bvec, g.Nc, n0, kbeg, kend, tid, ga);
   }
   for (int k0 = kbeg; k0 < kend; k0 += BK) {
     OA::stash(ra, As, tid);
     OW::stash(rw, Bs, tid);
     __syncthreads();
     if (k0 + BK < kend) {
-      OA::fetch(ra, abase, 0, g.lda, g.avec, g.M, m0, k0 + BK, kend, tid);
-      OW::fetch(rw, wbase, g.w_krows, g.ldw, g.bvec, g.Nc, n0, k0 + BK, kend, tid);
+      OA::fetch(ra, abase, 0, g.lda, g.avec, g.M, m0, k0 + BK, kend, tid, ga);
+      OW::fetch(rw, wbase, g.w_krows, g.ldw, g.bvec, g.Nc, n0, k0 + BK, kend, tid, ga);
     }
 #pragma unroll
     for (int ks = 0; ks < BK / M_::KC; ++ks) {
@@ -147,8 +199,8 @@ __global__ __launch_bounds__(256) void gemm_grad_kernel(GradGemmArgs g) {
       typename M_::frag af[2], bfr[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        af[i] = M_::load(&As[(wm * 64 + i * 32 + (lane & 31)) * LDS_STRIDE + kk]);
-        bfr[i] = M_::load(&Bs[(wn * 64 + i * 32 + (lane & 31)) * LDS_STRIDE + kk]);
+        af[i] = M_::load(&As[lds_off<T>(wm * 64 + i * 32 + (lane & 31), kk)]);
+        bfr[i] = M_::load(&Bs[lds_off<T>(wn * 64 + i * 32 + (lane & 31), kk)]);
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i)
@@ -178,20 +230,25 @@ __global__ __launch_bounds__(256) void gemm_grad_kernel(GradGemmArgs g) {
   }
 }
 
-template <typename T>
-int launch_grad_t(const GradGemmArgs& g, hipStream_t s) {
-  dim3 grid(((g.Nc + BN - 1) / BN) * ((g.M + BM - 1) / BM) * g.splits);
-  if (g.amode == GG_ROWS && g.wmode == GG_ROWS)
-    hipLaunchKernelGGL((gemm_grad_kernel<T, GG_ROWS, GG_ROWS>), grid, dim3(256), 0, s, g);
-  else if (g.amode == GG_ROWS && g.wmode == GG_TRANS)
-    hipLaunchKernelGGL((gemm_grad_kernel<T, GG_ROWS, GG_TRANS>), grid, dim3(256), 0, s, g);
-  else if (g.amode == GG_TRANS && g.wmode == GG_TRANS)
-    hipLaunchKernelGGL((gemm_grad_kernel<T, GG_TRANS, GG_TRANS>), grid, dim3(256), 0, s, g);
-  else if (g.amode == GG_TRANS && g.wmode == GG_ROWS)
-    hipLaunchKernelGGL((gemm_grad_kernel<T, GG_TRANS, GG_ROWS>), grid, dim3(256), 0, s, g);
+template <typename T, int AM>
+int launch_grad_w(const GradGemmArgs& g, dim3 grid, hipStream_t s) {
+  if (g.wmode == GG_ROWS)
+    hipLaunchKernelGGL((gemm_grad_kernel<T, AM, GG_ROWS>), grid, dim3(256), 0, s, g);
+  else if (g.wmode == GG_TRANS)
+    hipLaunchKernelGGL((gemm_grad_kernel<T, AM, GG_TRANS>), grid, dim3(256), 0, s, g);
+  else if (g.wmode == GG_GATHER_T)
+    hipLaunchKernelGGL((gemm_grad_kernel<T, AM, GG_GATHER_T>), grid, dim3(256), 0, s, g);
   else
     return CNNA_ERR_OPTION;
   return (int)hipGetLastError();
+}
+
+template <typename T>
+int launch_grad_t(const GradGemmArgs& g, hipStream_t s) {
+  dim3 grid(((g.Nc + BN - 1) / BN) * ((g.M + BM - 1) / BM) * g.splits);
+  if (g.amode == GG_ROWS) return launch_grad_w<T, GG_ROWS>(g, grid, s);
+  if (g.amode == GG_TRANS) return launch_grad_w<T, GG_TRANS>(g, grid, s);
+  return CNNA_ERR_OPTION;
 }
 
 template <typename T>
@@ -225,10 +282,16 @@ int launch_gemm_grad(int dtype, const GradGemmArgs& g0, hipStream_t s) {
   if (g.kchunk < bk) g.kchunk = bk;
   // 16-byte loads need 16-byte aligned rows
   g.avec = ((uintptr_t)g.a % 16 == 0) && ((g.lda * es) % 16 == 0);
-  bool bv = (g.ldw * es) % 16 == 0;
-  for (int i = 0; i < 3; ++i) bv = bv && ((uintptr_t)g.w[i] % 16 == 0);
-  g.bvec = bv;
-  if (g.w_krows == 0) g.w[1] = g.w[2] = g.w[0];
+  if (g.wmode == GG_GATHER_T) {
+    if (!g.g_idx || !g.g_w || g.g_K <= 0 || g.g_N <= 0 || g.g_din <= 0) return CNNA_ERR_NULL;
+    const int ce = 16 / es;
+    g.bvec = ((uintptr_t)g.w[0] % 16 == 0) && (g.g_din % ce == 0) && (g.g_dkp % ce == 0);
+  } else {
+    bool bv = (g.ldw * es) % 16 == 0;
+    if (g.w_krows == 0) g.w[1] = g.w[2] = g.w[0];
+    for (int i = 0; i < 3; ++i) bv = bv && ((uintptr_t)g.w[i] % 16 == 0);
+    g.bvec = bv;
+  }
   if (dtype == CNNA_BF16) return launch_grad_t<uint16_t>(g, s);
   if (dtype == CNNA_F32) return launch_grad_t<float>(g, s);
   return CNNA_ERR_DTYPE;

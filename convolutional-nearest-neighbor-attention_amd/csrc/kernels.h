@@ -91,10 +91,12 @@ int launch_permute_w0(int dtype, const void* w0, void* w0p, int dout, int din, i
 // Gradient GEMM: out[m][n] = sum_k A[m][k] * W[n][k] with
 //   A: ROWS a[m * lda + k]  |  TRANS a[k * lda + m]
 //   W: ROWS w[n * ldw + k]  |  TRANS w[k * ldw + n], optionally three
-//      matrices stacked along k (w_krows rows each).
+//      matrices stacked along k (w_krows rows each)
+//      | GATHER_T  W[n][k] = g_w[k*g_K + r] * w[0][(k - k % g_N + g_idx[k*g_K + r]) * g_dkp + c]
+//        with n = r*g_din + c: the gathered conv input P of token k, read transposed.
 // Without part: T into o (splits must be 1).  With part: fp32 partial sums
 // part[s][m][n] over k-chunks of kchunk, summed by launch_splitk_reduce.
-enum { GG_ROWS = 0, GG_TRANS = 1 };
+enum { GG_ROWS = 0, GG_TRANS = 1, GG_GATHER_T = 2 };
 struct GradGemmArgs {
   int M, Nc, Kd;
   const void* a;
@@ -104,6 +106,9 @@ struct GradGemmArgs {
   int64_t ldw;
   int wmode;
   int w_krows;       // 0: single W; else rows of k per stacked pointer
+  const int32_t* g_idx;
+  const float* g_w;
+  int g_K, g_N, g_din, g_dkp;
   void* o;
   int64_t ldo;
   float* part;
@@ -136,10 +141,6 @@ int launch_splitk_reduce(int dtype, const ReduceArgs& r, hipStream_t s);
 // Inverse head merge: dy (BH, N, dk) token-major from dZ (B, N, C).
 int launch_unmerge(int dtype, const void* dz, void* dy, int BH, int N, int dk, int H, int C,
                    hipStream_t s);
-
-// P[m][r*din + c] = w[m, r] * v[idx[m, r], c]  (materialised gathered input, standard conv)
-int launch_gather_p(int dtype, const void* v, const int32_t* idx, const float* w, void* P, int BH,
-                    int N, int K, int din, int dkp, hipStream_t s);
 
 // Per token: neighbour-weight gradient, softmax / weight backward, similarity
 // gradient coefficients and the key gradient; depthwise-weight partial sums.
