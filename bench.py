@@ -45,6 +45,58 @@ CONFIGS = {
 TRAIN = {"c5"}
 
 
+STAGE_KERNELS = {  # bench stage -> substring of the HIP kernel name
+    "select": "select_kernel",
+    "aggregate": "agg_kernel",
+    "project": "gemm_kernel<unsigned short, 0, 1",
+    "output_proj": "gemm_kernel<unsigned short, 0, 0",
+}
+
+
+def summarize_pmc(config, fetch_dir, write_dir):
+    """Turn two ``rocprofv3 --pmc FETCH_SIZE`` / ``--pmc WRITE_SIZE`` runs of this
+    script into HBM bytes per launch (profiles/traffic.json).  Each counter is
+    scaled by what it reads for the calibration copy of COPY_BYTES (the largest
+    copy kernel of the run)."""
+    import csv
+    import glob
+
+    def load(d, counter):
+        per = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] != counter:
+                    continue
+                per.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]) * 1024.0)
+        return per
+
+    out = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        per = load(d, counter)
+        copies = [max(v) for k, v in per.items() if "copy" in k.lower()]
+        if not copies:
+            raise SystemExit(f"no copy kernel in the {counter} run")
+        factor = max(copies) / COPY_BYTES
+        for stage, pat in STAGE_KERNELS.items():
+            vals = [x for k, v in per.items() if pat in k for x in v]
+            if not vals:
+                continue
+            e = out.setdefault(stage, {"kernel": pat})
+            e[counter.lower() + "_bytes"] = sorted(vals)[len(vals) // 2] / factor
+            e[counter.lower() + "_factor"] = round(factor, 4)
+    for e in out.values():
+        e["bytes_per_launch"] = round(e.get("fetch_size_bytes", 0.0) + e.get("write_size_bytes", 0.0))
+    try:
+        with open(TRAFFIC_FILE) as f:
+            allt = json.load(f)
+    except (OSError, ValueError):
+        allt = {}
+    allt[config] = out
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(allt, f, indent=1, sort_keys=True)
+    print(json.dumps(out, indent=1))
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -53,7 +105,36 @@ def parse():
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-sample-batch", type=int, default=8)
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write profiles/traffic.json from two rocprofv3 --pmc runs of this script")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+COPY_BYTES = 256 << 20   # calibration copy: reads and writes exactly this many bytes
+
+
+def calibration_copy(dev):
+    """One plain device copy of COPY_BYTES, run before the timed region so a
+    ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` pass over this script sees a
+    kernel of known traffic next to the operator's kernels (the scale factor
+    for the counters)."""
+    src = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def measured_traffic(config, kernel):
+    """HBM bytes per launch of the dominant kernel from the committed counter
+    summary (profiles/traffic.json), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return t[config][kernel]["bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def flops_of(B, N, Nq, C, H, K, conv):
@@ -67,6 +148,9 @@ def flops_of(B, N, Nq, C, H, K, conv):
 
 def main():
     args = parse()
+    if args.summarize_pmc:
+        summarize_pmc(args.config, *args.summarize_pmc)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU figures are not part of it",
                           "n_gpus": args.gpus}))
@@ -83,6 +167,7 @@ def main():
     m.train(train)
     x = torch.randn(B, N, C, device=dev).to(dtype)
     Nq = N if sampling == "all" else ns
+    calibration_copy(dev)
 
     # ---- whole-layer timing
     if train:
@@ -150,11 +235,13 @@ def main():
     if bound == "mfma":
         achieved = amount / t_s / 1e12
         roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": peak_mfma,
-                "unit": "TFLOP/s", "frac": round(achieved / peak_mfma, 4), "traffic": None}
+                "unit": "TFLOP/s", "frac": round(achieved / peak_mfma, 4),
+                "traffic": measured_traffic(args.config, dom)}
     else:
         achieved = amount / t_s / 1e9
         roof = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None}
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                "traffic": measured_traffic(args.config, dom)}
 
     total_flops = proj_f + sim_f + conv_f
     if train:
