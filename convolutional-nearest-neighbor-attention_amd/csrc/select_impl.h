@@ -6,11 +6,12 @@
 // similarity never reaches HBM.
 //
 // Block = 4 waves; a wave owns 32 tokens of one (batch, head).  Candidate
-// (query) tiles of 64 rows are staged through LDS, double buffered, and each
-// wave computes S^T for its tokens with v_mfma_f32_32x32x{16 bf16|2 f32}: the
-// A operand is the candidate tile and the B operand the wave's 32 key rows
-// (kept in registers), so lane l holds 16 candidates of token l % 32 per
-// 32-candidate block; lanes l and l + 32 split a token's candidates.
+// (query) tiles of TJ = 32 rows are staged through LDS, double buffered, and
+// each wave computes S^T for its tokens with v_mfma_f32_32x32x{16 bf16|2 f32}:
+// the A operand is the candidate tile and the B operand the wave's 32 key rows
+// (kept in registers), so lane l holds 16 candidates of token l % 32 per tile;
+// lanes l and l + 32 split a token's candidates.  The small tile keeps the
+// register and LDS footprint low enough for three blocks per CU at d_k = 128.
 //
 // Ranking key (larger is better):
 //   matmul / cosine, sampling 'all': the raw accumulator k.q (the positive
@@ -27,10 +28,13 @@
 //     half-lanes' lists is a lower bound tau of the token's K-th key, because
 //     it is attained by K distinct candidates.
 //  2. the tiles are recomputed and every key >= tau is appended to a per-lane
-//     LDS queue (about K + few entries per token).  Queues are merged into a
-//     sorted (key, index) register list when they fill and at the end; after a
-//     merge tau rises to just above the list's K-th key.  The two half-lane
-//     lists are finally merged and written out with the neighbour weights.
+//     LDS queue (about K + few entries per token).  When a queue fills, and at
+//     the end, the lower half-lane merges both half-lanes' queues into the
+//     token's one sorted (key, index) list in LDS; tau then rises to just
+//     above the list's K-th key for both halves.  Drains happen at tile
+//     positions where both halves have consumed a prefix of the candidate
+//     indices, so a later candidate never ties its way in ahead of a listed
+//     one.  The list is written out with the neighbour weights.
 #pragma once
 #include <type_traits>
 
@@ -39,7 +43,9 @@
 
 namespace {
 
-constexpr int TJ = 64;      // candidates per tile (two MFMA blocks)
+constexpr int TJ = 32;      // candidates per tile (one 32-row MFMA block)
+constexpr int NB = TJ / 32; // MFMA blocks per tile
+constexpr int TPB = 128;    // tokens per block
 constexpr int QC = 16;      // queue capacity per lane (drained when a lane passes QC - 8)
 constexpr int NT = 256;     // threads per block
 
@@ -96,7 +102,8 @@ CNNA_DEV float pick(const float (&L)[KMAX], int r) {
 // KFR: registers per lane holding the key rows (NCH fragments).
 template <int KFR, int KMAX, bool EUC, bool SMP>
 constexpr int sel_min_blocks() {
-  return (KMAX <= 16 && KFR <= 32 && ((!EUC && !SMP) || KFR * KMAX <= 288)) ? 2 : 1;
+  return (KMAX <= 16 && (KFR <= 32 || (KFR <= 64 && !EUC && !SMP)) &&
+          ((!EUC && !SMP) || KFR * KMAX <= 288)) ? 2 : 1;
 }
 
 template <typename T, int NCH, bool EXACT, int KMAX, bool EUC, bool SMP>
@@ -112,7 +119,7 @@ void select_kernel(SelArgs a) {
   const int total = a.BH * a.rb_per_bh;
   const int w = xcd_swizzle(blockIdx.x, total);
   const int bh = w / a.rb_per_bh, rb = w - bh * a.rb_per_bh;
-  const int ti = rb * 128 + wave * 32 + col;
+  const int ti = rb * TPB + wave * 32 + col;
   const bool tvalid = ti < a.N;
   const int tic = tvalid ? ti : a.N - 1;
 
@@ -177,19 +184,20 @@ void select_kernel(SelArgs a) {
   };
 
   // S^T tile for this wave: acc[blk][v] = k_ti . q_{j0 + blk*32 + mfma_row(v)}
-  auto compute = [&](int buf, f32x16_t (&acc)[2]) __attribute__((always_inline)) {
+  auto compute = [&](int buf, f32x16_t (&acc)[NB]) __attribute__((always_inline)) {
     const T* base = qt + buf * TJ * QS + col * QS + half * M_::KL;
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       if (EXACT || c < nch) {
-        const typename M_::frag a0 = M_::load(base + c * M_::KC);
-        const typename M_::frag a1 = M_::load(base + 32 * QS + c * M_::KC);
-        acc[0] = M_::mma(a0, kf[c], acc[0]);
-        acc[1] = M_::mma(a1, kf[c], acc[1]);
+        typename M_::frag af[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) af[b] = M_::load(base + b * 32 * QS + c * M_::KC);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[b] = M_::mma(af[b], kf[c], acc[b]);
       }
     }
   };
@@ -213,7 +221,7 @@ void select_kernel(SelArgs a) {
   // every wave is done with tile t, and tile t+3 is fetched into registers.
   // process(acc, buf, j0) consumes one tile's accumulators.
   auto sweep = [&](auto&& process) __attribute__((always_inline)) {
-    f32x16_t accA[2], accB[2];
+    f32x16_t accA[NB], accB[NB];
     fetch(0);
     stash(0);
     if (ntiles > 1) {
@@ -223,7 +231,7 @@ void select_kernel(SelArgs a) {
     __syncthreads();
     if (ntiles > 2) fetch(2);
     compute(0, accA);
-    auto step = [&](f32x16_t (&cur)[2], f32x16_t (&nxt)[2], int t) __attribute__((always_inline)) {
+    auto step = [&](f32x16_t (&cur)[NB], f32x16_t (&nxt)[NB], int t) __attribute__((always_inline)) {
       if (t + 1 < ntiles) compute((t + 1) & 1, nxt);
       process(cur, t & 1, t * TJ);
       if (!RAW) __syncthreads();       // process() read this tile's LDS side data
@@ -239,15 +247,18 @@ void select_kernel(SelArgs a) {
     }
   };
 
-  // Each lane's sorted (key, index) list lives in LDS (column tid of lk/li):
-  // only the drains and the final merge touch it, so it is not held in
-  // registers across the tile loop.  Index 0xffff marks an empty slot.
+  // Each token's sorted (key, index) list lives in LDS (column `slot` of
+  // lk/li), owned by the lower half-lane: only the drains and the output
+  // touch it.  Index 0xffff marks an empty slot.
+  const int slot = wave * 32 + col;
   float* lk = reinterpret_cast<float*>(qidx + QC * NT);
-  uint16_t* li = reinterpret_cast<uint16_t*>(lk + KMAX * NT);
+  uint16_t* li = reinterpret_cast<uint16_t*>(lk + KMAX * TPB);
+  if (half == 0) {
 #pragma unroll
-  for (int r = 0; r < KMAX; ++r) {
-    lk[r * NT + tid] = -INFINITY;
-    li[r * NT + tid] = 0xffff;
+    for (int r = 0; r < KMAX; ++r) {
+      lk[r * TPB + slot] = -INFINITY;
+      li[r * TPB + slot] = 0xffff;
+    }
   }
 
   if (a.Ksel > 0) {
@@ -256,10 +267,10 @@ void select_kernel(SelArgs a) {
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) L[r] = -INFINITY;
     // MASKED: the tile runs past Nq (only the last one); its extra rows drop out
-    auto bound_tile = [&](const f32x16_t (&acc)[2], int buf, int j0, auto MASKED)
+    auto bound_tile = [&](const f32x16_t (&acc)[NB], int buf, int j0, auto MASKED)
                           __attribute__((always_inline)) {
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
+      for (int b = 0; b < NB; ++b) {
         float key[16];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -274,7 +285,7 @@ void select_kernel(SelArgs a) {
         bound_insert<KMAX>(L, gm);
       }
     };
-    sweep([&](const f32x16_t (&acc)[2], int buf, int j0) __attribute__((always_inline)) {
+    sweep([&](const f32x16_t (&acc)[NB], int buf, int j0) __attribute__((always_inline)) {
       if (j0 + TJ <= a.Nq)
         bound_tile(acc, buf, j0, std::false_type{});
       else
@@ -293,35 +304,45 @@ void select_kernel(SelArgs a) {
     int cnt = 0;
     float* myk = qkey + tid;
     uint16_t* myi = qidx + tid;
+    // both half-lanes' queues go into the token's list; only the lower half works
     auto drain = [&]() __attribute__((always_inline)) {
-      float SV[KMAX];
-      int SI[KMAX];
+      const int cntp = __shfl_xor(cnt, 32);
+      float ntau = tau;
+      if (half == 0) {
+        float SV[KMAX];
+        int SI[KMAX];
 #pragma unroll
-      for (int r = 0; r < KMAX; ++r) {
-        SV[r] = lk[r * NT + tid];
-        const int j = li[r * NT + tid];
-        SI[r] = (j == 0xffff) ? 0x7fffffff : j;
-      }
-      for (int e = 0; __any(e < cnt); ++e) {
-        // lanes past their count insert a sentinel, which never moves the list
-        const bool live = e < cnt;
-        const float v = live ? myk[e * NT] : -INFINITY;
-        const int j = live ? (int)myi[e * NT] : 0x7fffffff;
-        list_insert<KMAX>(SV, SI, v, j);
-      }
+        for (int r = 0; r < KMAX; ++r) {
+          SV[r] = lk[r * TPB + slot];
+          const int j = li[r * TPB + slot];
+          SI[r] = (j == 0xffff) ? 0x7fffffff : j;
+        }
+        const int n = cnt > cntp ? cnt : cntp;
+        for (int e = 0; __any(e < n); ++e) {
+          // lanes past a count insert a sentinel, which never moves the list
+          const bool l0 = e < cnt, l1 = e < cntp;
+          const float v0 = l0 ? myk[e * NT] : -INFINITY;
+          const int j0 = l0 ? (int)myi[e * NT] : 0x7fffffff;
+          const float v1 = l1 ? myk[e * NT + 32] : -INFINITY;
+          const int j1 = l1 ? (int)myi[e * NT + 32] : 0x7fffffff;
+          list_insert<KMAX>(SV, SI, v0, j0);
+          list_insert<KMAX>(SV, SI, v1, j1);
+        }
 #pragma unroll
-      for (int r = 0; r < KMAX; ++r) {
-        lk[r * NT + tid] = SV[r];
-        li[r * NT + tid] = (uint16_t)(SI[r] == 0x7fffffff ? 0xffff : SI[r]);
+        for (int r = 0; r < KMAX; ++r) {
+          lk[r * TPB + slot] = SV[r];
+          li[r * TPB + slot] = (uint16_t)(SI[r] == 0x7fffffff ? 0xffff : SI[r]);
+        }
+        const int kth = pick<KMAX>(SI, a.Ksel - 1);
+        if (kth != 0x7fffffff) ntau = fmaxf(ntau, next_up(pick<KMAX>(SV, a.Ksel - 1)));
       }
+      tau = __shfl(ntau, lane & 31);
       cnt = 0;
-      const int kth = pick<KMAX>(SI, a.Ksel - 1);
-      if (kth != 0x7fffffff) tau = fmaxf(tau, next_up(pick<KMAX>(SV, a.Ksel - 1)));
     };
-    auto filter_tile = [&](const f32x16_t (&acc)[2], int buf, int j0, auto MASKED)
+    auto filter_tile = [&](const f32x16_t (&acc)[NB], int buf, int j0, auto MASKED)
                            __attribute__((always_inline)) {
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
+      for (int b = 0; b < NB; ++b) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           if (v % 8 == 0 && __any(cnt > QC - 8)) drain();
@@ -336,7 +357,7 @@ void select_kernel(SelArgs a) {
         }
       }
     };
-    sweep([&](const f32x16_t (&acc)[2], int buf, int j0) __attribute__((always_inline)) {
+    sweep([&](const f32x16_t (&acc)[NB], int buf, int j0) __attribute__((always_inline)) {
       if (j0 + TJ <= a.Nq)
         filter_tile(acc, buf, j0, std::false_type{});
       else
@@ -345,8 +366,7 @@ void select_kernel(SelArgs a) {
     drain();
   }
 
-  // ---------------- merge the two half-lane lists and write out
-  __syncthreads();
+  // ---------------- write the token's list out
   if (half == 0 && tvalid) {
     const int64_t o = ((int64_t)bh * a.N + ti) * a.K;
     int off = 0;
@@ -355,17 +375,10 @@ void select_kernel(SelArgs a) {
       a.vals[o] = 1.0f;
       off = 1;
     }
-    int ia = 0, ib = 0;
     for (int r = 0; r < a.Ksel; ++r) {
-      const int ra = ia < KMAX ? ia : KMAX - 1, rb2 = ib < KMAX ? ib : KMAX - 1;
-      const float va = lk[ra * NT + tid], vb = lk[rb2 * NT + tid + 32];
-      const int ja0 = li[ra * NT + tid], jb0 = li[rb2 * NT + tid + 32];
-      const int ja = ja0 == 0xffff ? 0x7fffffff : ja0, jb = jb0 == 0xffff ? 0x7fffffff : jb0;
-      const bool ta = (ia < KMAX) && (ib >= KMAX || better(va, ja, vb, jb));
-      const float key = ta ? va : vb;
-      const int j = ta ? ja : jb;
-      ia += ta ? 1 : 0;
-      ib += ta ? 0 : 1;
+      const float key = lk[r * TPB + slot];
+      const int j0 = li[r * TPB + slot];
+      const int j = j0 == 0xffff ? 0 : j0;
       float val = RAW ? key * a.kscale : key;
       int tok = j;
       if (SMP) tok = a.cand[j];
@@ -430,7 +443,7 @@ int launch_select_t(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
   const int nch0 = a.dkp / Mfma<T>::KC;
   const bool exact = nch0 == SelCfg<T>::MAXCH / 4 || nch0 == SelCfg<T>::MAXCH / 2 || nch0 == SelCfg<T>::MAXCH;
   const int kmax = !exact ? 32 : (a.Ksel <= 9 ? 9 : (a.Ksel <= 16 ? 16 : 32));
-  const size_t lists = (size_t)kmax * NT * (sizeof(float) + sizeof(uint16_t));
+  const size_t lists = (size_t)kmax * TPB * (sizeof(float) + sizeof(uint16_t));
   const size_t smem = 2 * TJ * (a.dkp + SelCfg<T>::VEC) * sizeof(T) + 2 * TJ * (sizeof(float) + sizeof(int)) +
                       queue + lists;
   dim3 grid(a.BH * a.rb_per_bh);
