@@ -46,7 +46,8 @@ namespace {
 constexpr int TJ = 32;      // candidates per tile (one 32-row MFMA block)
 constexpr int NB = TJ / 32; // MFMA blocks per tile
 constexpr int TPB = 128;    // tokens per block
-constexpr int QC = 16;      // queue capacity per lane (drained when a lane passes QC - 8)
+constexpr int QC = 12;      // queue capacity per lane (drained when a lane passes QC - QCHK)
+constexpr int QCHK = 4;     // elements between queue checks
 constexpr int NT = 256;     // threads per block
 
 template <typename T> struct SelCfg;
@@ -129,8 +130,8 @@ void select_kernel(SelArgs a) {
   T* qt = reinterpret_cast<T*>(smem);
   float* qnt = reinterpret_cast<float*>(smem + 2 * TJ * QS * sizeof(T));
   int* cdt = reinterpret_cast<int*>(qnt + 2 * TJ);
-  float* qkey = reinterpret_cast<float*>(cdt + 2 * TJ);
-  uint16_t* qidx = reinterpret_cast<uint16_t*>(qkey + QC * NT);
+  // queue entries: (key bits, candidate index) pairs, one 8-byte write per element
+  uint2* qent = reinterpret_cast<uint2*>(cdt + 2 * TJ);
 
   const T* Kb = static_cast<const T*>(a.k) + ((int64_t)bh * a.N + tic) * dkp;
   const T* Qb = static_cast<const T*>(a.q) + (int64_t)bh * a.Nq * dkp;
@@ -251,7 +252,7 @@ void select_kernel(SelArgs a) {
   // lk/li), owned by the lower half-lane: only the drains and the output
   // touch it.  Index 0xffff marks an empty slot.
   const int slot = wave * 32 + col;
-  float* lk = reinterpret_cast<float*>(qidx + QC * NT);
+  float* lk = reinterpret_cast<float*>(qent + QC * NT);
   uint16_t* li = reinterpret_cast<uint16_t*>(lk + KMAX * TPB);
   if (half == 0) {
 #pragma unroll
@@ -302,8 +303,7 @@ void select_kernel(SelArgs a) {
 
     // ---------------- pass 2: filter + queue
     int cnt = 0;
-    float* myk = qkey + tid;
-    uint16_t* myi = qidx + tid;
+    uint2* myq = qent + tid;
     // both half-lanes' queues go into the token's list; only the lower half works
     auto drain = [&]() __attribute__((always_inline)) {
       const int cntp = __shfl_xor(cnt, 32);
@@ -321,10 +321,11 @@ void select_kernel(SelArgs a) {
         for (int e = 0; __any(e < n); ++e) {
           // lanes past a count insert a sentinel, which never moves the list
           const bool l0 = e < cnt, l1 = e < cntp;
-          const float v0 = l0 ? myk[e * NT] : -INFINITY;
-          const int j0 = l0 ? (int)myi[e * NT] : 0x7fffffff;
-          const float v1 = l1 ? myk[e * NT + 32] : -INFINITY;
-          const int j1 = l1 ? (int)myi[e * NT + 32] : 0x7fffffff;
+          const uint2 q0 = myq[e * NT], q1 = myq[e * NT + 32];
+          const float v0 = l0 ? __uint_as_float(q0.x) : -INFINITY;
+          const int j0 = l0 ? (int)q0.y : 0x7fffffff;
+          const float v1 = l1 ? __uint_as_float(q1.x) : -INFINITY;
+          const int j1 = l1 ? (int)q1.y : 0x7fffffff;
           list_insert<KMAX>(SV, SI, v0, j0);
           list_insert<KMAX>(SV, SI, v1, j1);
         }
@@ -345,14 +346,13 @@ void select_kernel(SelArgs a) {
       for (int b = 0; b < NB; ++b) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          if (v % 8 == 0 && __any(cnt > QC - 8)) drain();
+          if (v % QCHK == 0 && __any(cnt > QC - QCHK)) drain();
           const int jl = b * 32 + mfma_row(v, lane);
           float key = keyof(acc[b][v], buf, jl);
           if (decltype(MASKED)::value && j0 + jl >= a.Nq) key = __builtin_nanf("");
           // branch-free append: write at the current slot, keep it only if it passed
-          // (cnt <= QC - 1 here: the block starts with cnt <= QC - 16)
-          myk[cnt * NT] = key;
-          myi[cnt * NT] = (uint16_t)(j0 + jl);
+          // (cnt <= QC - 1 here: a check precedes every QCHK elements)
+          myq[cnt * NT] = make_uint2(__float_as_uint(key), (uint32_t)(j0 + jl));
           cnt += (key >= tau) ? 1 : 0;
         }
       }
@@ -439,7 +439,7 @@ int launch_select_t(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
   if (a.dkp % Mfma<T>::KC != 0 || a.dkp > SelCfg<T>::MAXCH * Mfma<T>::KC || a.dkp % SelCfg<T>::VEC != 0)
     return CNNA_ERR_SHAPE;
   if (a.Nq > 65536) return CNNA_ERR_SHAPE;
-  const size_t queue = (size_t)QC * NT * (sizeof(float) + sizeof(uint16_t));
+  const size_t queue = (size_t)QC * NT * sizeof(uint2);
   const int nch0 = a.dkp / Mfma<T>::KC;
   const bool exact = nch0 == SelCfg<T>::MAXCH / 4 || nch0 == SelCfg<T>::MAXCH / 2 || nch0 == SelCfg<T>::MAXCH;
   const int kmax = !exact ? 32 : (a.Ksel <= 9 ? 9 : (a.Ksel <= 16 ? 16 : 32));
