@@ -73,11 +73,15 @@ CNNA_DEV void list_insert(float (&SV)[KMAX], int (&SI)[KMAX], float v, int j) {
   SI[0] = b[0] ? j : SI[0];
 }
 
+// max(a, b) for non-NaN inputs as one v_med3_f32 (fmaxf would first
+// canonicalise both operands, two more VALU ops)
+CNNA_DEV float max2(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, INFINITY); }
+
 template <int KMAX>
 CNNA_DEV void bound_insert(float (&L)[KMAX], float x) {
 #pragma unroll
   for (int r = KMAX - 1; r >= 1; --r) L[r] = __builtin_amdgcn_fmed3f(L[r - 1], x, L[r]);
-  L[0] = fmaxf(L[0], x);
+  L[0] = max2(L[0], x);
 }
 
 // L[r] for a runtime (wave-uniform) r, written as masked ORs so the
@@ -130,8 +134,9 @@ void select_kernel(SelArgs a) {
   T* qt = reinterpret_cast<T*>(smem);
   float* qnt = reinterpret_cast<float*>(smem + 2 * TJ * QS * sizeof(T));
   int* cdt = reinterpret_cast<int*>(qnt + 2 * TJ);
-  // queue entries: (key bits, candidate index) pairs, one 8-byte write per element
-  uint2* qent = reinterpret_cast<uint2*>(cdt + 2 * TJ);
+  // queue: key bits [QC][NT] followed by candidate indices [QC][NT]; the two
+  // stores of an append share one address (ds_write2st64_b32)
+  uint32_t* qent = reinterpret_cast<uint32_t*>(cdt + 2 * TJ);
 
   const T* Kb = static_cast<const T*>(a.k) + ((int64_t)bh * a.N + tic) * dkp;
   const T* Qb = static_cast<const T*>(a.q) + (int64_t)bh * a.Nq * dkp;
@@ -252,7 +257,7 @@ void select_kernel(SelArgs a) {
   // lk/li), owned by the lower half-lane: only the drains and the output
   // touch it.  Index 0xffff marks an empty slot.
   const int slot = wave * 32 + col;
-  float* lk = reinterpret_cast<float*>(qent + QC * NT);
+  float* lk = reinterpret_cast<float*>(qent + 2 * QC * NT);
   uint16_t* li = reinterpret_cast<uint16_t*>(lk + KMAX * TPB);
   if (half == 0) {
 #pragma unroll
@@ -279,10 +284,10 @@ void select_kernel(SelArgs a) {
           key[v] = keyof(acc[b][v], buf, jl);
           if (decltype(MASKED)::value && j0 + jl >= a.Nq) key[v] = -INFINITY;
         }
+        // keys here are finite or -inf (masked rows, negative euclidean d^2)
         float gm = key[0];
 #pragma unroll
-        for (int v = 1; v < 15; v += 2) gm = __builtin_fmaxf(gm, __builtin_fmaxf(key[v], key[v + 1]));
-        gm = __builtin_fmaxf(gm, key[15]);
+        for (int v = 1; v < 16; ++v) gm = max2(gm, key[v]);
         bound_insert<KMAX>(L, gm);
       }
     };
@@ -302,10 +307,12 @@ void select_kernel(SelArgs a) {
     float tau = pick<KMAX>(L, a.Ksel - 1);
 
     // ---------------- pass 2: filter + queue
-    int cnt = 0;
-    uint2* myq = qent + tid;
+
+    uint32_t* myq = qent + tid;
+    int woff = 0;   // cnt * NT: offset of this lane's next queue slot
     // both half-lanes' queues go into the token's list; only the lower half works
     auto drain = [&]() __attribute__((always_inline)) {
+      const int cnt = (int)((unsigned)woff / NT);
       const int cntp = __shfl_xor(cnt, 32);
       float ntau = tau;
       if (half == 0) {
@@ -321,11 +328,10 @@ void select_kernel(SelArgs a) {
         for (int e = 0; __any(e < n); ++e) {
           // lanes past a count insert a sentinel, which never moves the list
           const bool l0 = e < cnt, l1 = e < cntp;
-          const uint2 q0 = myq[e * NT], q1 = myq[e * NT + 32];
-          const float v0 = l0 ? __uint_as_float(q0.x) : -INFINITY;
-          const int j0 = l0 ? (int)q0.y : 0x7fffffff;
-          const float v1 = l1 ? __uint_as_float(q1.x) : -INFINITY;
-          const int j1 = l1 ? (int)q1.y : 0x7fffffff;
+          const float v0 = l0 ? __uint_as_float(myq[e * NT]) : -INFINITY;
+          const int j0 = l0 ? (int)myq[e * NT + QC * NT] : 0x7fffffff;
+          const float v1 = l1 ? __uint_as_float(myq[e * NT + 32]) : -INFINITY;
+          const int j1 = l1 ? (int)myq[e * NT + 32 + QC * NT] : 0x7fffffff;
           list_insert<KMAX>(SV, SI, v0, j0);
           list_insert<KMAX>(SV, SI, v1, j1);
         }
@@ -338,7 +344,7 @@ void select_kernel(SelArgs a) {
         if (kth != 0x7fffffff) ntau = fmaxf(ntau, next_up(pick<KMAX>(SV, a.Ksel - 1)));
       }
       tau = __shfl(ntau, lane & 31);
-      cnt = 0;
+      woff = 0;
     };
     auto filter_tile = [&](const f32x16_t (&acc)[NB], int buf, int j0, auto MASKED)
                            __attribute__((always_inline)) {
@@ -346,14 +352,15 @@ void select_kernel(SelArgs a) {
       for (int b = 0; b < NB; ++b) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          if (v % QCHK == 0 && __any(cnt > QC - QCHK)) drain();
+          if (v % QCHK == 0 && __any(woff > (QC - QCHK) * NT)) drain();
           const int jl = b * 32 + mfma_row(v, lane);
           float key = keyof(acc[b][v], buf, jl);
           if (decltype(MASKED)::value && j0 + jl >= a.Nq) key = __builtin_nanf("");
           // branch-free append: write at the current slot, keep it only if it passed
-          // (cnt <= QC - 1 here: a check precedes every QCHK elements)
-          myq[cnt * NT] = make_uint2(__float_as_uint(key), (uint32_t)(j0 + jl));
-          cnt += (key >= tau) ? 1 : 0;
+          // (slot <= QC - 1 here: a check precedes every QCHK elements)
+          myq[woff] = __float_as_uint(key);
+          myq[woff + QC * NT] = (uint32_t)(j0 + jl);
+          woff += (key >= tau) ? NT : 0;
         }
       }
     };
@@ -439,7 +446,7 @@ int launch_select_t(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
   if (a.dkp % Mfma<T>::KC != 0 || a.dkp > SelCfg<T>::MAXCH * Mfma<T>::KC || a.dkp % SelCfg<T>::VEC != 0)
     return CNNA_ERR_SHAPE;
   if (a.Nq > 65536) return CNNA_ERR_SHAPE;
-  const size_t queue = (size_t)QC * NT * sizeof(uint2);
+  const size_t queue = (size_t)QC * NT * 2 * sizeof(uint32_t);
   const int nch0 = a.dkp / Mfma<T>::KC;
   const bool exact = nch0 == SelCfg<T>::MAXCH / 4 || nch0 == SelCfg<T>::MAXCH / 2 || nch0 == SelCfg<T>::MAXCH;
   const int kmax = !exact ? 32 : (a.Ksel <= 9 ? 9 : (a.Ksel <= 16 ? 16 : 32));
