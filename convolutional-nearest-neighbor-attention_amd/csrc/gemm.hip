@@ -220,35 +220,52 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
           *reinterpret_cast<uint2*>(&Cs[ml * CP + nl]) = u;
         }
     __syncthreads();
+    // thread -> fixed 8-column group nl, rows ml = (tid >> 4) + 16 * it: the
+    // head-split coordinates are derived once and stepped, not divided per row
+    const int nl = (tid & 15) * 8;
+    const int n = n0 + nl;
+    int mat = 0, hh = 0, cc = n, b = 0, r = 0;
+    bool whole = n + 8 <= g.Nc;
+    if (OMODE == GEMM_O_HEADSPLIT) {
+      mat = n / g.ncol_each;
+      const int nn = n - mat * g.ncol_each;
+      hh = nn / g.o_dk;
+      cc = nn - hh * g.o_dk;
+      whole = whole && (cc + 8 <= g.o_dk);
+      const int m = m0 + (tid >> 4);
+      b = m / g.o_rows;
+      r = m - b * g.o_rows;
+    }
+    T* obase = static_cast<T*>(g.o[OMODE == GEMM_O_HEADSPLIT ? (mat > 2 ? 2 : mat) : 0]);
 #pragma unroll
     for (int it = 0; it < (BM * BN / 8) / 256; ++it) {
-      const int e = tid + it * 256;
-      const int ml = e >> 4, nl = (e & 15) * 8;
-      const int m = m0 + ml, n = n0 + nl;
+      const int ml = (tid >> 4) + it * 16;
+      const int m = m0 + ml;
+      if (it > 0 && OMODE == GEMM_O_HEADSPLIT) {
+        r += 16;
+        while (r >= g.o_rows) {
+          r -= g.o_rows;
+          ++b;
+        }
+      }
       if (m >= g.M || n >= g.Nc) continue;
       const u32x4_t val = *reinterpret_cast<const u32x4_t*>(&Cs[ml * CP + nl]);
       T* dst;
-      bool whole = n + 8 <= g.Nc;
-      if (OMODE == GEMM_O_HEADSPLIT) {
-        const int mat = n / g.ncol_each, nn = n - mat * g.ncol_each;
-        const int h = nn / g.o_dk, c = nn - h * g.o_dk;
-        const int b = m / g.o_rows, r = m - b * g.o_rows;
-        dst = static_cast<T*>(g.o[mat]) + (((int64_t)b * g.o_H + h) * g.o_rows + r) * g.o_dkp + c;
-        whole = whole && (c + 8 <= g.o_dk);
-      } else {
-        dst = static_cast<T*>(g.o[0]) + (int64_t)m * g.ldo + n;
-      }
+      if (OMODE == GEMM_O_HEADSPLIT)
+        dst = obase + (((int64_t)b * g.o_H + hh) * g.o_rows + r) * g.o_dkp + cc;
+      else
+        dst = obase + (int64_t)m * g.ldo + n;
       if (whole) {
         *reinterpret_cast<u32x4_t*>(dst) = val;
       } else {
+        // tile or head edge: element by element (rare)
         for (int u = 0; u < 8 && n + u < g.Nc; ++u) {
           const T v = Cs[ml * CP + nl + u];
           if (OMODE == GEMM_O_HEADSPLIT) {
             const int nu = n + u;
-            const int mat = nu / g.ncol_each, nn = nu - mat * g.ncol_each;
+            const int mt = nu / g.ncol_each, nn = nu - mt * g.ncol_each;
             const int h = nn / g.o_dk, c = nn - h * g.o_dk;
-            const int b = m / g.o_rows, r = m - b * g.o_rows;
-            static_cast<T*>(g.o[mat])[(((int64_t)b * g.o_H + h) * g.o_rows + r) * g.o_dkp + c] = v;
+            static_cast<T*>(g.o[mt])[(((int64_t)b * g.o_H + h) * g.o_rows + r) * g.o_dkp + c] = v;
           } else {
             dst[u] = v;
           }
