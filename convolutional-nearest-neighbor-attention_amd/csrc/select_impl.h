@@ -117,6 +117,9 @@ void select_kernel(SelArgs a) {
   using M_ = Mfma<T>;
   constexpr int VEC = SelCfg<T>::VEC;
   constexpr bool RAW = !EUC && !SMP;     // keys are raw accumulators
+  // short MFMA work per tile (d <= 128): predicated appends measured faster;
+  // wider heads hide the branch-free stores behind the longer MFMA chain
+  constexpr bool PRED_APPEND = NCH * Mfma<T>::KC <= 128;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -356,11 +359,20 @@ void select_kernel(SelArgs a) {
           const int jl = b * 32 + mfma_row(v, lane);
           float key = keyof(acc[b][v], buf, jl);
           if (decltype(MASKED)::value && j0 + jl >= a.Nq) key = __builtin_nanf("");
-          // branch-free append: write at the current slot, keep it only if it passed
           // (slot <= QC - 1 here: a check precedes every QCHK elements)
-          myq[woff] = __float_as_uint(key);
-          myq[woff + QC * NT] = (uint32_t)(j0 + jl);
-          woff += (key >= tau) ? NT : 0;
+          if (PRED_APPEND) {
+            // store the passers only; element steps where no lane passes skip it
+            if (key >= tau) {
+              myq[woff] = __float_as_uint(key);
+              myq[woff + QC * NT] = (uint32_t)(j0 + jl);
+              woff += NT;
+            }
+          } else {
+            // branch-free: write at the current slot, keep it only if it passed
+            myq[woff] = __float_as_uint(key);
+            myq[woff + QC * NT] = (uint32_t)(j0 + jl);
+            woff += (key >= tau) ? NT : 0;
+          }
         }
       }
     };
