@@ -103,12 +103,13 @@ CNNA_DEV float pick(const float (&L)[KMAX], int r) {
 
 // NCH: number of MFMA reduction chunks (d / KC); EXACT: the head width equals
 // NCH * KC (no per-chunk guards), otherwise NCH is an upper bound.
-// Two blocks (8 waves) per CU where the register footprint allows it without spills.
+// Three or two blocks per CU where the register footprint allows it without spills.
 // KFR: registers per lane holding the key rows (NCH fragments).
 template <int KFR, int KMAX, bool EUC, bool SMP>
 constexpr int sel_min_blocks() {
-  return (KMAX <= 16 && (KFR <= 32 || (KFR <= 64 && !EUC && !SMP)) &&
-          ((!EUC && !SMP) || KFR * KMAX <= 288)) ? 2 : 1;
+  return (KMAX <= 9 && KFR <= 32 && !EUC && !SMP) ? 3
+         : (KMAX <= 16 && (KFR <= 32 || (KFR <= 64 && !EUC && !SMP)) &&
+            ((!EUC && !SMP) || KFR * KMAX <= 288)) ? 2 : 1;
 }
 
 template <typename T, int NCH, bool EXACT, int KMAX, bool EUC, bool SMP>
@@ -159,10 +160,16 @@ void select_kernel(SelArgs a) {
 
   // ---- tile staging: unconditional loads of clamped rows (rows >= Nq are
   // masked when keys are formed), so no load sits behind a branch
-  u32x4_t pf[NPF];
-  float pfn = 0.0f;
-  int pfc = 0;
-  auto fetch = [&](int tile) __attribute__((always_inline)) {
+  // PD register sets: tile t+2 is loaded PD steps before it is stashed, which
+  // covers the load latency when a step is short (narrow heads)
+  constexpr int PD = NPF <= 1 ? 2 : 1;
+  u32x4_t pfs[PD][NPF];
+  float pfns[PD] = {};
+  int pfcs[PD] = {};
+  auto fetch = [&](int tile, auto SLOT) __attribute__((always_inline)) {
+    u32x4_t (&pf)[NPF] = pfs[decltype(SLOT)::value];
+    float& pfn = pfns[decltype(SLOT)::value];
+    int& pfc = pfcs[decltype(SLOT)::value];
     const int j0 = tile * TJ;
 #pragma unroll
     for (int i = 0; i < NPF; ++i) {
@@ -178,7 +185,10 @@ void select_kernel(SelArgs a) {
       if (SMP) pfc = a.cand[j];
     }
   };
-  auto stash = [&](int buf) __attribute__((always_inline)) {
+  auto stash = [&](int buf, auto SLOT) __attribute__((always_inline)) {
+    const u32x4_t (&pf)[NPF] = pfs[decltype(SLOT)::value];
+    const float pfn = pfns[decltype(SLOT)::value];
+    const int pfc = pfcs[decltype(SLOT)::value];
     T* dst = qt + buf * TJ * QS;
 #pragma unroll
     for (int i = 0; i < NPF; ++i) {
@@ -230,29 +240,34 @@ void select_kernel(SelArgs a) {
   // every wave is done with tile t, and tile t+3 is fetched into registers.
   // process(acc, buf, j0) consumes one tile's accumulators.
   auto sweep = [&](auto&& process) __attribute__((always_inline)) {
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, PD - 1>;
     f32x16_t accA[NB], accB[NB];
-    fetch(0);
-    stash(0);
+    fetch(0, S0{});
+    stash(0, S0{});
     if (ntiles > 1) {
-      fetch(1);
-      stash(1);
+      fetch(1, S1{});
+      stash(1, S1{});
     }
     __syncthreads();
-    if (ntiles > 2) fetch(2);
+    if (ntiles > 2) fetch(2, S0{});
+    if (PD == 2 && ntiles > 3) fetch(3, S1{});
     compute(0, accA);
-    auto step = [&](f32x16_t (&cur)[NB], f32x16_t (&nxt)[NB], int t) __attribute__((always_inline)) {
+    // step over tile t (t even: buffer / register slot 0, t odd: 1)
+    auto step = [&](f32x16_t (&cur)[NB], f32x16_t (&nxt)[NB], int t, auto SLOT)
+                    __attribute__((always_inline)) {
       if (t + 1 < ntiles) compute((t + 1) & 1, nxt);
       process(cur, t & 1, t * TJ);
       if (!RAW) __syncthreads();       // process() read this tile's LDS side data
       if (t + 2 < ntiles) {
-        stash(t & 1);
-        if (t + 3 < ntiles) fetch(t + 3);
+        stash(t & 1, SLOT);
+        if (t + 2 + PD < ntiles) fetch(t + 2 + PD, SLOT);
       }
       __syncthreads();
     };
     for (int t = 0; t < ntiles; t += 2) {
-      step(accA, accB, t);
-      if (t + 1 < ntiles) step(accB, accA, t + 1);
+      step(accA, accB, t, S0{});
+      if (t + 1 < ntiles) step(accB, accA, t + 1, S1{});
     }
   };
 
@@ -385,49 +400,60 @@ void select_kernel(SelArgs a) {
     drain();
   }
 
-  // ---------------- write the token's list out
+  // ---------------- write the token's list out (values kept in registers)
   if (half == 0 && tvalid) {
     const int64_t o = ((int64_t)bh * a.N + ti) * a.K;
-    int off = 0;
+    constexpr int OFF = SMP ? 1 : 0;
+    constexpr int KO = KMAX + OFF;
+    float vv[KO];
+    int tk[KO];
     if (SMP) {
-      a.idx[o] = ti;
-      a.vals[o] = 1.0f;
-      off = 1;
+      tk[0] = ti;
+      vv[0] = 1.0f;
     }
-    for (int r = 0; r < a.Ksel; ++r) {
+#pragma unroll
+    for (int r = 0; r < KMAX; ++r) {
       const float key = lk[r * TPB + slot];
       const int j0 = li[r * TPB + slot];
-      const int j = j0 == 0xffff ? 0 : j0;
+      const int j = (j0 == 0xffff || r >= a.Ksel) ? 0 : j0;
       float val = RAW ? key * a.kscale : key;
       int tok = j;
       if (SMP) tok = a.cand[j];
       if (EUC) val = (key == -INFINITY) ? __builtin_nanf("") : sqrtf(-key);
       if (SMP && EUC && tok == ti) val = a.mask_val;
-      a.idx[o + off + r] = tok;
-      a.vals[o + off + r] = val;
+      vv[OFF + r] = val;
+      tk[OFF + r] = tok;
+    }
+#pragma unroll
+    for (int r = 0; r < KO; ++r) {
+      if (r < a.K) {
+        a.idx[o + r] = tk[r];
+        a.vals[o + r] = vv[r];
+      }
     }
     // neighbour weights (layers.py:352-355, 382-385, 394-397, 426-429)
     if (a.w != nullptr) {
+      float wv[KO];
       if (a.softmax) {
         float mx = -INFINITY;
-        for (int r = 0; r < a.K; ++r) {
-          const float v = a.vals[o + r];
-          mx = fmaxf(mx, EUC ? -v : v);
-        }
+#pragma unroll
+        for (int r = 0; r < KO; ++r)
+          if (r < a.K) mx = fmaxf(mx, EUC ? -vv[r] : vv[r]);
         float sum = 0.0f;
-        for (int r = 0; r < a.K; ++r) {
-          const float v = a.vals[o + r];
-          const float e = expf((EUC ? -v : v) - mx);
-          a.w[o + r] = e;
-          sum += e;
+#pragma unroll
+        for (int r = 0; r < KO; ++r) {
+          wv[r] = (r < a.K) ? expf((EUC ? -vv[r] : vv[r]) - mx) : 0.0f;
+          sum += wv[r];
         }
-        for (int r = 0; r < a.K; ++r) a.w[o + r] = a.w[o + r] / sum;
+#pragma unroll
+        for (int r = 0; r < KO; ++r) wv[r] = wv[r] / sum;
       } else {
-        for (int r = 0; r < a.K; ++r) {
-          const float v = a.vals[o + r];
-          a.w[o + r] = EUC ? 1.0f / (v + 1e-8f) : v;
-        }
+#pragma unroll
+        for (int r = 0; r < KO; ++r) wv[r] = EUC ? 1.0f / (vv[r] + 1e-8f) : vv[r];
       }
+#pragma unroll
+      for (int r = 0; r < KO; ++r)
+        if (r < a.K) a.w[o + r] = wv[r];
     }
   }
 }
