@@ -54,23 +54,29 @@ template <typename T> struct SelCfg;
 template <> struct SelCfg<uint16_t> { static constexpr int MAXCH = 16, VEC = 8; };  // d <= 256
 template <> struct SelCfg<float> { static constexpr int MAXCH = 64, VEC = 4; };     // d <= 128
 
-// (v, j) ranks before (ov, oj): larger key, then lower index (branch-free)
-CNNA_DEV bool better(float v, int j, float ov, int oj) {
-  return (v > ov) | ((v == ov) & (j < oj));
+// A (key, index) pair as one 64-bit integer ordered like the ranking (larger
+// key first, then lower index): high word = order-preserving image of the float key, low word = ~index.
+// 0 (below every real entry) marks an empty list slot.
+CNNA_DEV uint32_t ord_key(float f) {
+  const uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+CNNA_DEV float key_of_ord(uint32_t u) {
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+CNNA_DEV uint64_t pack_entry(float key, uint32_t j) {
+  return ((uint64_t)ord_key(key) << 32) | (uint64_t)(~j);
 }
 
+// insert x into the descending list L (one 64-bit compare per slot)
 template <int KMAX>
-CNNA_DEV void list_insert(float (&SV)[KMAX], int (&SI)[KMAX], float v, int j) {
+CNNA_DEV void list_insert(uint64_t (&L)[KMAX], uint64_t x) {
   bool b[KMAX];
 #pragma unroll
-  for (int r = 0; r < KMAX; ++r) b[r] = better(v, j, SV[r], SI[r]);
+  for (int r = 0; r < KMAX; ++r) b[r] = x > L[r];
 #pragma unroll
-  for (int r = KMAX - 1; r >= 1; --r) {
-    SV[r] = b[r - 1] ? SV[r - 1] : (b[r] ? v : SV[r]);
-    SI[r] = b[r - 1] ? SI[r - 1] : (b[r] ? j : SI[r]);
-  }
-  SV[0] = b[0] ? v : SV[0];
-  SI[0] = b[0] ? j : SI[0];
+  for (int r = KMAX - 1; r >= 1; --r) L[r] = b[r - 1] ? L[r - 1] : (b[r] ? x : L[r]);
+  L[0] = b[0] ? x : L[0];
 }
 
 // max(a, b) for non-NaN inputs as one v_med3_f32 (fmaxf would first
@@ -92,6 +98,17 @@ CNNA_DEV int pick(const int (&L)[KMAX], int r) {
 #pragma unroll
   for (int i = 0; i < KMAX; ++i) t |= L[i] & -(int)(i == r);
   return t;
+}
+template <int KMAX>
+CNNA_DEV uint64_t pick(const uint64_t (&L)[KMAX], int r) {
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i) {
+    const uint32_t m = -(uint32_t)(i == r);
+    lo |= (uint32_t)L[i] & m;
+    hi |= (uint32_t)(L[i] >> 32) & m;
+  }
+  return ((uint64_t)hi << 32) | lo;
 }
 template <int KMAX>
 CNNA_DEV float pick(const float (&L)[KMAX], int r) {
@@ -271,18 +288,14 @@ void select_kernel(SelArgs a) {
     }
   };
 
-  // Each token's sorted (key, index) list lives in LDS (column `slot` of
-  // lk/li), owned by the lower half-lane: only the drains and the output
-  // touch it.  Index 0xffff marks an empty slot.
+  // Each token's sorted list of packed entries lives in LDS (column `slot`
+  // of lst), owned by the lower half-lane: only the drains and the output
+  // touch it.  0 marks an empty slot.
   const int slot = wave * 32 + col;
-  float* lk = reinterpret_cast<float*>(qent + 2 * QC * NT);
-  uint16_t* li = reinterpret_cast<uint16_t*>(lk + KMAX * TPB);
+  uint64_t* lst = reinterpret_cast<uint64_t*>(qent + 2 * QC * NT);
   if (half == 0) {
 #pragma unroll
-    for (int r = 0; r < KMAX; ++r) {
-      lk[r * TPB + slot] = -INFINITY;
-      li[r * TPB + slot] = 0xffff;
-    }
+    for (int r = 0; r < KMAX; ++r) lst[r * TPB + slot] = 0;
   }
 
   if (a.Ksel > 0) {
@@ -334,32 +347,22 @@ void select_kernel(SelArgs a) {
       const int cntp = __shfl_xor(cnt, 32);
       float ntau = tau;
       if (half == 0) {
-        float SV[KMAX];
-        int SI[KMAX];
+        uint64_t L2[KMAX];
 #pragma unroll
-        for (int r = 0; r < KMAX; ++r) {
-          SV[r] = lk[r * TPB + slot];
-          const int j = li[r * TPB + slot];
-          SI[r] = (j == 0xffff) ? 0x7fffffff : j;
-        }
+        for (int r = 0; r < KMAX; ++r) L2[r] = lst[r * TPB + slot];
         const int n = cnt > cntp ? cnt : cntp;
         for (int e = 0; __any(e < n); ++e) {
-          // lanes past a count insert a sentinel, which never moves the list
-          const bool l0 = e < cnt, l1 = e < cntp;
-          const float v0 = l0 ? __uint_as_float(myq[e * NT]) : -INFINITY;
-          const int j0 = l0 ? (int)myq[e * NT + QC * NT] : 0x7fffffff;
-          const float v1 = l1 ? __uint_as_float(myq[e * NT + 32]) : -INFINITY;
-          const int j1 = l1 ? (int)myq[e * NT + 32 + QC * NT] : 0x7fffffff;
-          list_insert<KMAX>(SV, SI, v0, j0);
-          list_insert<KMAX>(SV, SI, v1, j1);
+          // lanes past a count insert 0, which never moves the list
+          const uint64_t x0 = (e < cnt) ? pack_entry(__uint_as_float(myq[e * NT]), myq[e * NT + QC * NT]) : 0;
+          const uint64_t x1 =
+              (e < cntp) ? pack_entry(__uint_as_float(myq[e * NT + 32]), myq[e * NT + 32 + QC * NT]) : 0;
+          list_insert<KMAX>(L2, x0);
+          list_insert<KMAX>(L2, x1);
         }
 #pragma unroll
-        for (int r = 0; r < KMAX; ++r) {
-          lk[r * TPB + slot] = SV[r];
-          li[r * TPB + slot] = (uint16_t)(SI[r] == 0x7fffffff ? 0xffff : SI[r]);
-        }
-        const int kth = pick<KMAX>(SI, a.Ksel - 1);
-        if (kth != 0x7fffffff) ntau = fmaxf(ntau, next_up(pick<KMAX>(SV, a.Ksel - 1)));
+        for (int r = 0; r < KMAX; ++r) lst[r * TPB + slot] = L2[r];
+        const uint64_t kth = pick<KMAX>(L2, a.Ksel - 1);
+        if (kth != 0) ntau = fmaxf(ntau, next_up(key_of_ord((uint32_t)(kth >> 32))));
       }
       tau = __shfl(ntau, lane & 31);
       woff = 0;
@@ -413,9 +416,9 @@ void select_kernel(SelArgs a) {
     }
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) {
-      const float key = lk[r * TPB + slot];
-      const int j0 = li[r * TPB + slot];
-      const int j = (j0 == 0xffff || r >= a.Ksel) ? 0 : j0;
+      const uint64_t ent = lst[r * TPB + slot];
+      const float key = key_of_ord((uint32_t)(ent >> 32));
+      const int j = (ent == 0 || r >= a.Ksel) ? 0 : (int)(~(uint32_t)ent);
       float val = RAW ? key * a.kscale : key;
       int tok = j;
       if (SMP) tok = a.cand[j];
@@ -488,7 +491,7 @@ int launch_select_t(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
   const int nch0 = a.dkp / Mfma<T>::KC;
   const bool exact = nch0 == SelCfg<T>::MAXCH / 4 || nch0 == SelCfg<T>::MAXCH / 2 || nch0 == SelCfg<T>::MAXCH;
   const int kmax = !exact ? 32 : (a.Ksel <= 9 ? 9 : (a.Ksel <= 16 ? 16 : 32));
-  const size_t lists = (size_t)kmax * TPB * (sizeof(float) + sizeof(uint16_t));
+  const size_t lists = (size_t)kmax * TPB * sizeof(uint64_t);
   const size_t smem = 2 * TJ * (a.dkp + SelCfg<T>::VEC) * sizeof(T) + 2 * TJ * (sizeof(float) + sizeof(int)) +
                       queue + lists;
   dim3 grid(a.BH * a.rb_per_bh);
