@@ -403,13 +403,12 @@ void select_kernel(SelArgs a) {
     drain();
   }
 
-  // ---------------- write the token's list out (values kept in registers)
+  // ---------------- the token's list -> idx, vals, w (values kept in registers)
+  constexpr int OFF = SMP ? 1 : 0;
+  constexpr int KO = KMAX + OFF;
+  float vv[KO], wv[KO];
+  int tk[KO];
   if (half == 0 && tvalid) {
-    const int64_t o = ((int64_t)bh * a.N + ti) * a.K;
-    constexpr int OFF = SMP ? 1 : 0;
-    constexpr int KO = KMAX + OFF;
-    float vv[KO];
-    int tk[KO];
     if (SMP) {
       tk[0] = ti;
       vv[0] = 1.0f;
@@ -427,38 +426,44 @@ void select_kernel(SelArgs a) {
       vv[OFF + r] = val;
       tk[OFF + r] = tok;
     }
-#pragma unroll
-    for (int r = 0; r < KO; ++r) {
-      if (r < a.K) {
-        a.idx[o + r] = tk[r];
-        a.vals[o + r] = vv[r];
-      }
-    }
     // neighbour weights (layers.py:352-355, 382-385, 394-397, 426-429)
-    if (a.w != nullptr) {
-      float wv[KO];
-      if (a.softmax) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < KO; ++r)
-          if (r < a.K) mx = fmaxf(mx, EUC ? -vv[r] : vv[r]);
-        float sum = 0.0f;
-#pragma unroll
-        for (int r = 0; r < KO; ++r) {
-          wv[r] = (r < a.K) ? expf((EUC ? -vv[r] : vv[r]) - mx) : 0.0f;
-          sum += wv[r];
-        }
-#pragma unroll
-        for (int r = 0; r < KO; ++r) wv[r] = wv[r] / sum;
-      } else {
-#pragma unroll
-        for (int r = 0; r < KO; ++r) wv[r] = EUC ? 1.0f / (vv[r] + 1e-8f) : vv[r];
-      }
+    if (a.softmax) {
+      float mx = -INFINITY;
 #pragma unroll
       for (int r = 0; r < KO; ++r)
-        if (r < a.K) a.w[o + r] = wv[r];
+        if (r < a.K) mx = fmaxf(mx, EUC ? -vv[r] : vv[r]);
+      float sum = 0.0f;
+#pragma unroll
+      for (int r = 0; r < KO; ++r) {
+        wv[r] = (r < a.K) ? expf((EUC ? -vv[r] : vv[r]) - mx) : 0.0f;
+        sum += wv[r];
+      }
+#pragma unroll
+      for (int r = 0; r < KO; ++r) wv[r] = wv[r] / sum;
+    } else {
+#pragma unroll
+      for (int r = 0; r < KO; ++r) wv[r] = EUC ? 1.0f / (vv[r] + 1e-8f) : vv[r];
     }
   }
+  // The block's tokens are consecutive, so each output is one contiguous run
+  // of nvalid * K values: staged through LDS (the queue region, free after the
+  // final drains) and stored by all threads with consecutive addresses.
+  uint32_t* stg = qent;
+  const int nvalid = min(TPB, a.N - rb * TPB);
+  const int64_t obase = ((int64_t)bh * a.N + rb * TPB) * a.K;
+  auto emit = [&](auto get, uint32_t* dst) __attribute__((always_inline)) {
+    __syncthreads();
+    if (half == 0 && tvalid) {
+#pragma unroll
+      for (int r = 0; r < KO; ++r)
+        if (r < a.K) stg[slot * a.K + r] = get(r);
+    }
+    __syncthreads();
+    for (int e = tid; e < nvalid * a.K; e += NT) dst[obase + e] = stg[e];
+  };
+  emit([&](int r) { return (uint32_t)tk[r]; }, reinterpret_cast<uint32_t*>(a.idx));
+  emit([&](int r) { return __float_as_uint(vv[r]); }, reinterpret_cast<uint32_t*>(a.vals));
+  if (a.w != nullptr) emit([&](int r) { return __float_as_uint(wv[r]); }, reinterpret_cast<uint32_t*>(a.w));
 }
 
 template <typename T, int NCH, bool EXACT, int KMAX>
@@ -487,6 +492,8 @@ int launch_select_t(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
   if (a.dkp % Mfma<T>::KC != 0 || a.dkp > SelCfg<T>::MAXCH * Mfma<T>::KC || a.dkp % SelCfg<T>::VEC != 0)
     return CNNA_ERR_SHAPE;
   if (a.Nq > 65536) return CNNA_ERR_SHAPE;
+  // the queue region also stages one output array (TPB * K <= TPB * 32 values) at the end
+  static_assert(TPB * 32 <= QC * NT * 2, "output staging must fit the queue region");
   const size_t queue = (size_t)QC * NT * 2 * sizeof(uint32_t);
   const int nch0 = a.dkp / Mfma<T>::KC;
   const bool exact = nch0 == SelCfg<T>::MAXCH / 4 || nch0 == SelCfg<T>::MAXCH / 2 || nch0 == SelCfg<T>::MAXCH;
