@@ -157,7 +157,8 @@ void select_kernel(SelArgs a) {
   int* cdt = reinterpret_cast<int*>(qnt + 2 * TJ);
   // queue: key bits [QC][NT] followed by candidate indices [QC][NT]; the two
   // stores of an append share one address (ds_write2st64_b32)
-  uint32_t* qent = reinterpret_cast<uint32_t*>(cdt + 2 * TJ);
+  int* dflag = cdt + 2 * TJ;   // [2][4] per-wave drain requests, by tile parity
+  uint32_t* qent = reinterpret_cast<uint32_t*>(dflag + 8);
 
   const T* Kb = static_cast<const T*>(a.k) + ((int64_t)bh * a.N + tic) * dkp;
   const T* Qb = static_cast<const T*>(a.q) + (int64_t)bh * a.Nq * dkp;
@@ -367,8 +368,18 @@ void select_kernel(SelArgs a) {
       tau = __shfl(ntau, lane & 31);
       woff = 0;
     };
+    // Drains are synchronised across the block: a wave that would otherwise
+    // drain on its own mid-tile stalls the other waves at the next barrier, so
+    // at every tile boundary all waves drain together when any lane of the
+    // block holds more than BTHR entries (flags written before the barrier).
+    constexpr int BTHR = 6;
     auto filter_tile = [&](const f32x16_t (&acc)[NB], int buf, int j0, auto MASKED)
                            __attribute__((always_inline)) {
+      const int t = j0 / TJ;
+      if (t > 0) {
+        const int* f = dflag + ((t - 1) & 1) * 4;
+        if (__any((f[0] | f[1] | f[2] | f[3]) != 0)) drain();
+      }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
 #pragma unroll
@@ -393,6 +404,8 @@ void select_kernel(SelArgs a) {
           }
         }
       }
+      const bool need = __any(woff > BTHR * NT);
+      if (lane == 0) dflag[(t & 1) * 4 + wave] = need ? 1 : 0;
     };
     sweep([&](const f32x16_t (&acc)[NB], int buf, int j0) __attribute__((always_inline)) {
       if (j0 + TJ <= a.Nq)
@@ -499,7 +512,7 @@ int launch_select_t(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
   const bool exact = nch0 == SelCfg<T>::MAXCH / 4 || nch0 == SelCfg<T>::MAXCH / 2 || nch0 == SelCfg<T>::MAXCH;
   const int kmax = !exact ? 32 : (a.Ksel <= 9 ? 9 : (a.Ksel <= 16 ? 16 : 32));
   const size_t lists = (size_t)kmax * TPB * sizeof(uint64_t);
-  const size_t smem = 2 * TJ * (a.dkp + SelCfg<T>::VEC) * sizeof(T) + 2 * TJ * (sizeof(float) + sizeof(int)) +
+  const size_t smem = 2 * TJ * (a.dkp + SelCfg<T>::VEC) * sizeof(T) + 2 * TJ * (sizeof(float) + sizeof(int)) + 8 * sizeof(int) +
                       queue + lists;
   dim3 grid(a.BH * a.rb_per_bh);
   const int nch = a.dkp / Mfma<T>::KC;
