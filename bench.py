@@ -41,6 +41,8 @@ CONFIGS = {
     "c4a": (128, 197, 192, 3, 9, torch.float32, "matmul", "depthwise", "random", 64, 2),
     "c4b": (128, 197, 192, 3, 9, torch.float32, "matmul", "depthwise", "spatial", 8, 2),
     "c5": (8, 4096, 768, 3, 16, torch.bfloat16, "matmul", "standard", "all", -1, 3),
+    # c2: the whole ViT-Tiny (12 blocks, N = 197) in run_vit; the layer shape is c2layer
+    "c2": (128, 197, 192, 3, 9, torch.bfloat16, "matmul", "depthwise", "all", -1, 0),
 }
 TRAIN = {"c5"}
 
@@ -146,6 +148,114 @@ def flops_of(B, N, Nq, C, H, K, conv):
     return proj, sim, cv
 
 
+def vit_cpu_baseline(model, imgs, args):
+    """The ViT on the host cores with every attention block replaced by the
+    oracle's restatement of the reference op sequence (bounded sample)."""
+    import copy
+
+    from oracle import cnna_oracle as O
+
+    class OracleAttention(torch.nn.Module):
+        def __init__(self, attn, cfg):
+            super().__init__()
+            self.p = O.Params.from_module_state({k: v.detach() for k, v in attn.state_dict().items()},
+                                                cfg.convolution_type)
+            self.cfg = cfg
+
+        def forward(self, x):
+            return O.forward(x, self.p, self.cfg, mode="reference")
+
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    cpu = copy.deepcopy(model).cpu()
+    a = cpu.args
+    cfg = O.Config(d_hidden=a.d_hidden, num_heads=a.num_heads, K=a.K, sampling_type=a.sampling_type,
+                   num_samples=a.num_samples, magnitude_type=a.magnitude_type, seq_length=197,
+                   convolution_type=a.convolution_type, softmax_topk_val=a.softmax_topk_val)
+    for blk in cpu.transformer_encoder:
+        blk.attention = OracleAttention(blk.attention, cfg)
+    bs = max(1, min(args.cpu_sample_batch, imgs.shape[0]))
+    x = imgs[:bs].cpu()
+    with torch.no_grad():
+        cpu(x)
+        reps, t = 0, 0.0
+        while reps < 3 or (t < 10.0 and reps < 20):
+            c0 = time.perf_counter()
+            cpu(x)
+            t += time.perf_counter() - c0
+            reps += 1
+    n_tok = bs * 197 * reps
+    return {"value": round(n_tok / t, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"{reps} ViT forwards of {bs} of {imgs.shape[0]} images in bf16, "
+                                      "attention = oracle reference-mode op sequence",
+            "affinity_cores": ncores, "os_cpu_count": os.cpu_count(), "torch": torch.__version__}
+
+
+def run_vit(args):
+    """c2: full ViT-Tiny forward (12 ConvNN-Attention blocks, B=128, 224x224, bf16)."""
+    import cnna_ops as ops
+    from vit import ViT, vit_tiny_args
+
+    torch.manual_seed(0)
+    model = ViT(vit_tiny_args()).to("cuda").to(torch.bfloat16).eval()
+    B = 128
+    imgs = torch.randn(B, 3, 224, 224, device="cuda").to(torch.bfloat16)
+    calibration_copy("cuda")
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            model(imgs)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            model(imgs)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / args.steps
+    tokens = B * 197
+    # dominant operator stage at the block shape, timed with HIP events
+    blk = model.transformer_encoder[0].attention
+    x = torch.randn(B, 197, 192, device="cuda").to(torch.bfloat16)
+    d = ops.make_desc(B, 197, 192, 3, 197, 9, 197, torch.bfloat16, "matmul", "depthwise",
+                      blk.softmax_topk_val, False, False)
+    ts = []
+    with torch.no_grad():
+        q, k, v, qn, kn = ops.project_qkv(d, x, None, blk.W_q.weight, blk.W_k.weight, blk.W_v.weight)
+        for it in range(args.warmup + args.steps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            ops.select(d, k, q, kn, qn, None)
+            e1.record()
+            if it >= args.warmup:
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1))
+    t_sel = sorted(ts)[len(ts) // 2] / 1e3
+    f_sim = 2 * B * 197 * 197 * 192
+    achieved = f_sim / t_sel / 1e12
+    # ViT-Tiny forward flops: patch embedding + 12 x (layer + MLP) + classifier
+    f_layer = 2 * B * 192 * 192 * 4 * 197 + f_sim + 2 * B * 197 * 192 * 9
+    f_mlp = 2 * 2 * B * 197 * 192 * 768
+    f_total = 2 * B * 196 * 192 * 768 + 12 * (f_layer + f_mlp) + 2 * B * 192 * 10
+    cpu = None if args.no_cpu else vit_cpu_baseline(model, imgs, args)
+    rec = {
+        "metric": "ConvNN-ViT-Tiny forward tokens/s (12 blocks, N=197, C=192, K=9, bf16)",
+        "value": round(tokens / (ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: images ~ N(0,1), random-init weights (seed 0)",
+        "config": {"workload": "c2: ViT-Tiny forward, 12 ConvNN-Attention blocks (matmul, depthwise, "
+                               "K=9, sampling all, softmax_topk_val=False as the CLI default), "
+                               "B=128 images 224x224, patch 16",
+                   "B": B, "N": 197, "C": 192, "H": 3, "K": 9, "layers": 12},
+        "roofline": {"kernel": "select", "bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic("c2", "select")},
+        "model": {"flops": f_total, "tflops": round(f_total / (ms / 1e3) / 1e12, 2)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def main():
     args = parse()
     if args.summarize_pmc:
@@ -155,6 +265,9 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU figures are not part of it",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.config == "c2":
+        run_vit(args)
+        return
     import cnna_ops as ops
     from layers import MultiHeadConvNNAttention
 
