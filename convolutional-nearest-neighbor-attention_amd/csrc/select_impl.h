@@ -23,7 +23,8 @@
 // Ties break by the lowest candidate index.
 //
 // Two passes over the candidates:
-//  1. per lane, the maximum of each 16-candidate group goes into a sorted
+//  1. per lane, the maximum of each 16-candidate group (4-candidate groups
+//     when Nq <= 512) goes into a sorted
 //     register list (med3 insertion); the K-th largest of the union of both
 //     half-lanes' lists is a lower bound tau of the token's K-th key, because
 //     it is attained by K distinct candidates.
@@ -302,6 +303,10 @@ void select_kernel(SelArgs a) {
   if (a.Ksel > 0) {
     // ---------------- pass 1: group-max bound
     float L[KMAX];
+    // Short rows (at most 16 tiles): groups of 4 candidates, so that tau is
+    // drawn from enough groups to sit close to the K-th key (fewer passers
+    // and queue drains in pass 2); long rows: groups of 16.
+    const bool fine = ntiles <= 16;
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) L[r] = -INFINITY;
     // MASKED: the tile runs past Nq (only the last one); its extra rows drop out
@@ -317,10 +322,16 @@ void select_kernel(SelArgs a) {
           if (decltype(MASKED)::value && j0 + jl >= a.Nq) key[v] = -INFINITY;
         }
         // keys here are finite or -inf (masked rows, negative euclidean d^2)
-        float gm = key[0];
+        if (fine) {
 #pragma unroll
-        for (int v = 1; v < 16; ++v) gm = max2(gm, key[v]);
-        bound_insert<KMAX>(L, gm);
+          for (int g = 0; g < 4; ++g)
+            bound_insert<KMAX>(L, max2(max2(key[4 * g], key[4 * g + 1]), max2(key[4 * g + 2], key[4 * g + 3])));
+        } else {
+          float gm = key[0];
+#pragma unroll
+          for (int v = 1; v < 16; ++v) gm = max2(gm, key[v]);
+          bound_insert<KMAX>(L, gm);
+        }
       }
     };
     sweep([&](const f32x16_t (&acc)[NB], int buf, int j0) __attribute__((always_inline)) {
