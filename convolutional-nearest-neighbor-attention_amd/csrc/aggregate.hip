@@ -23,8 +23,10 @@ namespace {
 
 template <typename T, int VW> struct Vec;
 template <> struct Vec<uint16_t, 8> {
-  static CNNA_DEV void load(const uint16_t* p, float (&o)[8]) {
-    const uint4 u = *reinterpret_cast<const uint4*>(p);
+  typedef uint4 Raw;
+  static CNNA_DEV Raw raw(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+  static CNNA_DEV void load(const uint16_t* p, float (&o)[8]) { unpack(raw(p), o); }
+  static CNNA_DEV void unpack(const uint4 u, float (&o)[8]) {
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -40,8 +42,10 @@ template <> struct Vec<uint16_t, 8> {
   }
 };
 template <> struct Vec<float, 4> {
-  static CNNA_DEV void load(const float* p, float (&o)[4]) {
-    const float4 u = *reinterpret_cast<const float4*>(p);
+  typedef float4 Raw;
+  static CNNA_DEV Raw raw(const float* p) { return *reinterpret_cast<const float4*>(p); }
+  static CNNA_DEV void load(const float* p, float (&o)[4]) { unpack(raw(p), o); }
+  static CNNA_DEV void unpack(const float4 u, float (&o)[4]) {
     o[0] = u.x; o[1] = u.y; o[2] = u.z; o[3] = u.w;
   }
   static CNNA_DEV void store(float* p, const float (&o)[4]) {
@@ -53,7 +57,9 @@ template <typename T> struct Vec<T, 1> {
   static CNNA_DEV void store(T* p, const float (&o)[1]) { stf(p, o[0]); }
 };
 
-template <typename T, int VW, bool COPY>
+// KM > 0: K <= KM, and all K neighbour rows of a token are loaded before
+// any is used (one memory latency per token instead of K)
+template <typename T, int VW, bool COPY, int KM>
 __global__ __launch_bounds__(256) void agg_kernel(AggArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x;
@@ -101,6 +107,23 @@ __global__ __launch_bounds__(256) void agg_kernel(AggArgs a) {
     float acc[VW];
     if (COPY) {
       Vec<T, VW>::load(static_cast<const T*>(a.v) + ((int64_t)bh * a.N + i) * dout + c0, acc);
+    } else if constexpr (KM > 0) {
+#pragma unroll
+      for (int u = 0; u < VW; ++u) acc[u] = 0.0f;
+      typename Vec<T, VW>::Raw raw[KM > 0 ? KM : 1];
+#pragma unroll
+      for (int r = 0; r < KM; ++r)
+        if (r < a.K) raw[r] = Vec<T, VW>::raw(V + (int64_t)sj[tt * a.K + r] * a.dkp + c0);
+#pragma unroll
+      for (int r = 0; r < KM; ++r) {
+        if (r < a.K) {
+          const float wr = sw[tt * a.K + r];
+          float vv[VW];
+          Vec<T, VW>::unpack(raw[r], vv);
+#pragma unroll
+          for (int u = 0; u < VW; ++u) acc[u] += sW[r * dout + c0 + u] * (wr * vv[u]);
+        }
+      }
     } else {
 #pragma unroll
       for (int u = 0; u < VW; ++u) acc[u] = 0.0f;
@@ -136,9 +159,26 @@ __global__ __launch_bounds__(256) void agg_kernel(AggArgs a) {
   if (!stage_z) return;
   __syncthreads();
 
-  // write the staged flat range into Z: lanes run along the columns a of a row t
+  // write the staged flat range into Z
   const int64_t F1 = (int64_t)(i0 + ntok) * dout;
   const int na = (int)((F1 - 1) / a.N) - a_lo + 1;
+  constexpr int ZV = 16 / sizeof(T);
+  if (F0 % a.N == 0 && F1 % a.N == 0 && na == ZV && (h * dout + a_lo) % ZV == 0 && a.C % ZV == 0) {
+    // the block covers ZV whole columns of Z (16 aligned bytes per row): a
+    // thread per row t gathers them from the ZV staged rows, one 16-byte store
+    T* Zb = static_cast<T*>(a.out) + (int64_t)b * a.N * a.C + h * dout + a_lo;
+    for (int t = tid; t < a.N; t += 256) {
+      union {
+        u32x4_t u;
+        T e[ZV];
+      } pk;
+#pragma unroll
+      for (int u = 0; u < ZV; ++u) pk.e[u] = stage[u * NP + t];
+      *reinterpret_cast<u32x4_t*>(Zb + (int64_t)t * a.C) = pk.u;
+    }
+    return;
+  }
+  // general case: lanes run along the columns a of a row t
   const int rows_per_it = 256 / na;
   const int ar = tid % na, trow = tid / na;
   if (trow >= rows_per_it) return;
@@ -182,10 +222,20 @@ int launch_vw(const AggArgs& a0, hipStream_t s) {
   a.ti = ti;
   a.nblk = (a.N + ti - 1) / ti;
   dim3 grid(a.BH * a.nblk);
+  if constexpr (!COPY) {
+    if (vec && a.K <= 9) {
+      hipLaunchKernelGGL((agg_kernel<T, V, COPY, 9>), grid, dim3(256), lds(ti), s, a);
+      return (int)hipGetLastError();
+    }
+    if (vec && a.K <= 16) {
+      hipLaunchKernelGGL((agg_kernel<T, V, COPY, 16>), grid, dim3(256), lds(ti), s, a);
+      return (int)hipGetLastError();
+    }
+  }
   if (vec)
-    hipLaunchKernelGGL((agg_kernel<T, V, COPY>), grid, dim3(256), lds(ti), s, a);
+    hipLaunchKernelGGL((agg_kernel<T, V, COPY, 0>), grid, dim3(256), lds(ti), s, a);
   else
-    hipLaunchKernelGGL((agg_kernel<T, 1, COPY>), grid, dim3(256), lds(ti), s, a);
+    hipLaunchKernelGGL((agg_kernel<T, 1, COPY, 0>), grid, dim3(256), lds(ti), s, a);
   return (int)hipGetLastError();
 }
 
