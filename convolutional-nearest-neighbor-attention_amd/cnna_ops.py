@@ -70,6 +70,8 @@ def _load():
         "cnna_core_backward_workspace": ([D], ctypes.c_size_t),
         "cnna_core_backward": ([D, P, I64, P, P, P, P, P, P, ctypes.POINTER(Saved), P,
                                 ctypes.POINTER(Grads), P, ctypes.c_size_t, P], I32),
+        "cnna_layernorm": ([I32, I64, I32, P, I64, P, I64, P, I64, P, P, ctypes.c_float, P, I64, P], I32),
+        "cnna_linear": ([I32, I64, I32, I32, P, I64, P, P, I32, P, I64, P, I64, P], I32),
     }
     for name, (args, res) in sigs.items():
         f = getattr(lib, name)
@@ -83,7 +85,8 @@ EXPORTED = ("cnna_abi_version", "cnna_error_string", "cnna_check_desc", "cnna_he
             "cnna_project_qkv", "cnna_select", "cnna_aggregate_workspace", "cnna_aggregate",
             "cnna_output_proj", "cnna_forward_workspace", "cnna_forward",
             "cnna_output_proj_backward_workspace", "cnna_output_proj_backward",
-            "cnna_core_backward_workspace", "cnna_core_backward")
+            "cnna_core_backward_workspace", "cnna_core_backward", "cnna_layernorm", "cnna_linear")
+ACT_NONE, ACT_GELU = 0, 1
 
 
 def check(status: int) -> None:
@@ -194,6 +197,47 @@ def forward_fused(d: Desc, x, cand, Wq, Wk, Wv, Wo, w0, w1=None):
                            _ptr(Wk.contiguous()), _ptr(Wv.contiguous()), _ptr(Wo.contiguous()),
                            _ptr(w0), _ptr(w1), _ptr(out), d.C, _ptr(ws), ws_bytes, _stream()))
     return out
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """(..., C) with unit stride in C -> (rows, C) view or contiguous copy."""
+    t2 = t.reshape(-1, t.shape[-1])
+    return t2 if t2.stride(-1) == 1 else t2.contiguous()
+
+
+def layernorm(x, weight, bias, eps, residual=None, want_sum=False):
+    """nn.LayerNorm over the last dimension of ``x`` (+ ``residual`` first).
+
+    Returns y, or (y, x + residual) with ``want_sum``.  Inference helper of
+    the ViT block (vit.py:247-248, 262-267); no autograd."""
+    xr = _rows(x)
+    rows, C = xr.shape
+    rr = None if residual is None else _rows(residual)
+    y = torch.empty((rows, C), dtype=x.dtype, device=x.device)
+    s = torch.empty_like(y) if (want_sum and residual is not None) else None
+    check(LIB.cnna_layernorm(dtype_code(x.dtype), rows, C, _ptr(xr), xr.stride(0), _ptr(rr),
+                             0 if rr is None else rr.stride(0), _ptr(s), 0 if s is None else s.stride(0),
+                             _ptr(None if weight is None else weight.contiguous()),
+                             _ptr(None if bias is None else bias.contiguous()), float(eps), _ptr(y),
+                             y.stride(0), _stream()))
+    y = y.view(x.shape)
+    if want_sum:
+        return y, (x if residual is None else s.view(x.shape))
+    return y
+
+
+def linear(a, W, bias=None, gelu=False, residual=None):
+    """act(a @ W^T + bias) + residual through the MFMA GEMM (nn.Linear with the
+    ViT block's epilogues fused: vit.py:253-257, 263-264, 269); no autograd."""
+    ar = _rows(a)
+    M, Kd = ar.shape
+    Nout = W.shape[0]
+    rr = None if residual is None else _rows(residual)
+    out = torch.empty((M, Nout), dtype=a.dtype, device=a.device)
+    check(LIB.cnna_linear(dtype_code(a.dtype), M, Nout, Kd, _ptr(ar), ar.stride(0), _ptr(W.contiguous()),
+                          _ptr(None if bias is None else bias.contiguous()), ACT_GELU if gelu else ACT_NONE,
+                          _ptr(rr), 0 if rr is None else rr.stride(0), _ptr(out), out.stride(0), _stream()))
+    return out.view(*a.shape[:-1], Nout)
 
 
 def output_proj_backward(d: Desc, z, Wo, dout):

@@ -245,6 +245,61 @@ int cnna_output_proj(const cnna_desc* d, const void* z, const void* Wo, void* ou
   return launch_gemm(d->dtype, GEMM_A_ROWS, GEMM_O_PLAIN, g, (hipStream_t)stream);
 }
 
+int cnna_layernorm(int32_t dtype, int64_t rows, int32_t C, const void* x, int64_t ldx, const void* res,
+                   int64_t ldr, void* sum_out, int64_t ld_sum, const void* gamma, const void* beta,
+                   float eps, void* y, int64_t ldy, void* stream) {
+  if (dtype != CNNA_F32 && dtype != CNNA_BF16) return CNNA_ERR_DTYPE;
+  if (rows < 0 || C <= 0 || C > 1024 || ldx < C || ldy < C || (res && ldr < C) || (sum_out && ld_sum < C))
+    return CNNA_ERR_SHAPE;
+  if (rows > 0 && (!x || !y)) return CNNA_ERR_NULL;
+  LnArgs a;
+  memset(&a, 0, sizeof(a));
+  a.x = x;
+  a.ldx = ldx;
+  a.res = res;
+  a.ldr = ldr;
+  a.sum_out = sum_out;
+  a.lds = ld_sum;
+  a.gamma = gamma;
+  a.beta = beta;
+  a.eps = eps;
+  a.y = y;
+  a.ldy = ldy;
+  a.rows = rows;
+  a.C = C;
+  return launch_layernorm(dtype, a, (hipStream_t)stream);
+}
+
+int cnna_linear(int32_t dtype, int64_t M, int32_t Nout, int32_t Kd, const void* a, int64_t lda,
+                const void* W, const void* bias, int32_t act, const void* res, int64_t ldr, void* out,
+                int64_t ldo, void* stream) {
+  if (dtype != CNNA_F32 && dtype != CNNA_BF16) return CNNA_ERR_DTYPE;
+  if (act != CNNA_ACT_NONE && act != CNNA_ACT_GELU) return CNNA_ERR_OPTION;
+  if (M < 0 || M > INT32_MAX || Nout <= 0 || Kd <= 0 || lda < Kd || ldo < Nout || (res && ldr < Nout))
+    return CNNA_ERR_SHAPE;
+  if (M == 0) return 0;
+  if (!a || !W || !out) return CNNA_ERR_NULL;
+  const int es = elem_size(dtype);
+  GemmArgs g;
+  memset(&g, 0, sizeof(g));
+  g.M = (int)M;
+  g.Nc = Nout;
+  g.Kd = Kd;
+  g.a = a;
+  g.lda = lda;
+  g.avec = ((Kd * es) % 16 == 0) && ((lda * es) % 16 == 0) && aligned16(a);
+  g.w[0] = W;
+  g.ncol_each = Nout;
+  g.bvec = ((Kd * es) % 16 == 0) && aligned16(W);
+  g.o[0] = out;
+  g.ldo = ldo;
+  g.bias = bias;
+  g.act = act == CNNA_ACT_GELU ? GEMM_ACT_GELU : GEMM_ACT_NONE;
+  g.res = res;
+  g.ldr = ldr;
+  return launch_gemm(dtype, GEMM_A_ROWS, GEMM_O_PLAIN, g, (hipStream_t)stream);
+}
+
 size_t cnna_forward_workspace(const cnna_desc* d) {
   if (cnna_check_desc(d)) return 0;
   const size_t es = elem_size(d->dtype), dkp = dkp_of(d), BH = (size_t)d->B * d->H;

@@ -45,6 +45,35 @@ CNNA_DEV u32x4_t scale_vec(u32x4_t s, float w, float) {
   return o;
 }
 
+// nn.GELU() (erf form): 0.5 x (1 + erf(x / sqrt 2)) with erf from Abramowitz &
+// Stegun, Handbook of Mathematical Functions (1964), formula 7.1.26:
+//   erfc(z) = (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),  t = 1 / (1 + p z),
+// absolute error <= 1.5e-7 for z >= 0.  For x < 0 the factor 1 + erf is erfc(|z|)
+// itself (no cancellation).  About a dozen VALU operations.
+CNNA_DEV float gelu_erf(float x) {
+  const float z = fabsf(x) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, z, 1.0f));
+  float p = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+  p = __builtin_fmaf(p, t, 1.421413741f);
+  p = __builtin_fmaf(p, t, -0.284496736f);
+  p = __builtin_fmaf(p, t, 0.254829592f);
+  const float erfc = p * t * __expf(-z * z);
+  return 0.5f * x * (x >= 0.0f ? 2.0f - erfc : erfc);
+}
+
+// Linear epilogue before the store: v + bias[n], then the activation.  For
+// bf16 the biased value is rounded to bf16 first, as the unfused nn.Linear ->
+// nn.GELU sequence rounds it.
+template <typename T>
+CNNA_DEV float lin_epi(const GemmArgs& g, float v, int n) {
+  if (g.bias != nullptr) v += ldf(static_cast<const T*>(g.bias) + n);
+  if (g.act == GEMM_ACT_GELU) {
+    if (sizeof(T) == 2) v = bf2f(f2bf(v));
+    v = gelu_erf(v);
+  }
+  return v;
+}
+
 // four consecutive outputs -> one 8-byte (bf16) or 16-byte (fp32) store
 CNNA_DEV void store4(uint16_t* p, float a, float b, float c, float d) {
   uint2 u;
@@ -214,9 +243,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
           const int ml = wm * 64 + i * 32 + (lane & 31);
           const int nl = wn * 64 + j * 32 + vq * 8 + (lane >> 5) * 4;
           const f32x16_t& a = acc[i][j];
+          float e[4] = {a[vq * 4], a[vq * 4 + 1], a[vq * 4 + 2], a[vq * 4 + 3]};
+          if (OMODE == GEMM_O_PLAIN && (g.bias != nullptr || g.act != GEMM_ACT_NONE)) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) e[u] = lin_epi<T>(g, e[u], min(n0 + nl + u, g.Nc - 1));
+          }
           uint2 u;
-          u.x = f2bf2(a[vq * 4], a[vq * 4 + 1]);
-          u.y = f2bf2(a[vq * 4 + 2], a[vq * 4 + 3]);
+          u.x = f2bf2(e[0], e[1]);
+          u.y = f2bf2(e[2], e[3]);
           *reinterpret_cast<uint2*>(&Cs[ml * CP + nl]) = u;
         }
     __syncthreads();
@@ -249,7 +283,15 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
         }
       }
       if (m >= g.M || n >= g.Nc) continue;
-      const u32x4_t val = *reinterpret_cast<const u32x4_t*>(&Cs[ml * CP + nl]);
+      u32x4_t val = *reinterpret_cast<const u32x4_t*>(&Cs[ml * CP + nl]);
+      if (OMODE == GEMM_O_PLAIN && g.res != nullptr && whole) {
+        // residual: bf16 linear output + bf16 residual, added in fp32 and rounded once
+        const u32x4_t r = *reinterpret_cast<const u32x4_t*>(static_cast<const T*>(g.res) + (int64_t)m * g.ldr + n);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          val[q] = f2bf2(__uint_as_float(val[q] << 16) + __uint_as_float(r[q] << 16),
+                         __uint_as_float(val[q] & 0xffff0000u) + __uint_as_float(r[q] & 0xffff0000u));
+      }
       T* dst;
       if (OMODE == GEMM_O_HEADSPLIT)
         dst = obase + (((int64_t)b * g.o_H + hh) * g.o_rows + r) * g.o_dkp + cc;
@@ -267,7 +309,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
             const int h = nn / g.o_dk, c = nn - h * g.o_dk;
             static_cast<T*>(g.o[mt])[(((int64_t)b * g.o_H + h) * g.o_rows + r) * g.o_dkp + c] = v;
           } else {
-            dst[u] = v;
+            if (g.res != nullptr)
+              stf(&dst[u], ldf(&v) + ldf(static_cast<const T*>(g.res) + (int64_t)m * g.ldr + n + u));
+            else
+              dst[u] = v;
           }
         }
       }
@@ -312,7 +357,20 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         if (!mok[i]) continue;
-        const f32x16_t& a = acc[i][j];
+        f32x16_t a = acc[i][j];
+        if (OMODE == GEMM_O_PLAIN && (g.bias != nullptr || g.act != GEMM_ACT_NONE || g.res != nullptr)) {
+          const int64_t rrow = (int64_t)(m0 + wm * 64 + i * 32 + (lane & 31)) * g.ldr;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int n = min(nq + u, g.Nc - 1);
+            float v = lin_epi<T>(g, a[vq * 4 + u], n);
+            if (g.res != nullptr) {
+              if (sizeof(T) == 2) v = bf2f(f2bf(v));
+              v += ldf(static_cast<const T*>(g.res) + rrow + n);
+            }
+            a[vq * 4 + u] = v;
+          }
+        }
         if (vec) {
           store4(ob + roff[i] + oc, a[vq * 4], a[vq * 4 + 1], a[vq * 4 + 2], a[vq * 4 + 3]);
         } else {
@@ -364,6 +422,7 @@ int launch_t(int amode, int omode, const GemmArgs& g0, hipStream_t s) {
   for (int i = 0; i < 3; ++i)
     if (g.o[i] && ((uintptr_t)g.o[i] % 16) != 0) ostage = false;
   if (omode == GEMM_O_PLAIN) ostage = ostage && (g.ldo % 8 == 0);
+  if (g.res != nullptr) ostage = ostage && ((uintptr_t)g.res % 16 == 0) && (g.ldr % 8 == 0);
   else ostage = ostage && (g.o_dkp % 8 == 0) && (g.ncol_each % 8 == 0) && (g.o_dk % 8 == 0);
   g.ostage = ostage;
   const bool fast = g.avec && g.bvec && (g.Kd % GemmCfg<T>::BK == 0);

@@ -32,9 +32,34 @@ struct GemmArgs {
   int avec, bvec;  // 16-byte vector loads allowed for A / W
   int ovec;        // set by the launcher: 4-column vector stores allowed
   int ostage;      // set by the launcher: bf16 tile staged through LDS for 16-byte stores
+  // plain output only (nn.Linear extras): out = act(A W^T + bias) + res
+  const void* bias;  // (Nc) or NULL
+  int act;           // GEMM_ACT_*
+  const void* res;   // (M, Nc) residual with row stride ldr, or NULL
+  int64_t ldr;
 };
+enum { GEMM_ACT_NONE = 0, GEMM_ACT_GELU = 1 };
 
 int launch_gemm(int dtype, int amode, int omode, const GemmArgs& g, hipStream_t s);
+
+// ---------------------------------------------------------------- ViT block
+// LayerNorm over rows of C (one wave per row), optional residual in front.
+struct LnArgs {
+  const void* x;
+  int64_t ldx;
+  const void* res;    // or NULL
+  int64_t ldr;
+  void* sum_out;      // x + res, or NULL
+  int64_t lds;
+  const void* gamma;  // or NULL
+  const void* beta;   // or NULL
+  float eps;
+  void* y;
+  int64_t ldy;
+  int64_t rows;
+  int C;
+};
+int launch_layernorm(int dtype, const LnArgs& a, hipStream_t s);
 
 // ---------------------------------------------------------------- prep
 // Per row of a head-split tensor: coordinate channel, zero padding, cosine

@@ -103,6 +103,12 @@ class MultiHeadConvNNAttention(nn.Module):
         return idx.to(torch.int32)
 
     def forward(self, x):
+        z, d = self.core(x)
+        return ops.OutputProj.apply(z, self.W_o.weight, d)
+
+    def core(self, x):
+        """Everything before W_o (layers.py:261-317): returns (z, desc), z the
+        merged conv output after dropout."""
         if x.dim() != 3:
             raise RuntimeError(f"expected x of shape (B, N, C), got {tuple(x.shape)}")
         if not x.is_cuda:
@@ -122,5 +128,4 @@ class MultiHeadConvNNAttention(nn.Module):
                                  True)
         # dropout on the conv output (layers.py:316); elementwise, so applying it
         # after the head merge is the same operation on permuted elements
-        z = self.dropout(z)
-        return ops.OutputProj.apply(z, self.W_o.weight, d)
+        return self.dropout(z), d

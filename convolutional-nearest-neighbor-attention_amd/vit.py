@@ -7,6 +7,11 @@ sinusoidal positional encoding, pre-norm transformer blocks whose attention is
 Module and parameter names follow the reference so state dicts carry over.
 Only ``layer="ConvNNAttention"`` is built here; the other attention families
 of the reference are outside this operator's scope and raise ValueError.
+
+In inference (eval mode, no gradients) each block runs with its prologue and
+epilogues fused: LayerNorm kernels, W_o + residual, fc1 + bias + GELU and
+fc2 + bias + residual in the GEMM epilogues (cnna_layernorm, cnna_linear).
+Training and autograd use the composable modules.
 """
 from __future__ import annotations
 
@@ -16,6 +21,7 @@ from types import SimpleNamespace
 import torch
 import torch.nn as nn
 
+import cnna_ops as ops
 from layers import MultiHeadConvNNAttention
 
 
@@ -42,6 +48,8 @@ class PatchEmbedding(nn.Module):
 
     def forward(self, x):
         x = self.flatten(self.linear_projection(x)).transpose(1, 2)
+        if x.is_cuda and not self.training and not torch.is_grad_enabled() and self.norm.weight.dtype == x.dtype:
+            return ops.layernorm(x, self.norm.weight, self.norm.bias, self.norm.eps)
         return self.norm(x)
 
 
@@ -84,8 +92,30 @@ class TransformerEncoder(nn.Module):
                                  nn.Linear(d_mlp, d_hidden))
 
     def forward(self, x):
+        if self._fusable(x):
+            return self._forward_fused(x)
         x = x + self.dropout1(self.attention(self.norm1(x)))
         return x + self.dropout2(self.mlp(self.norm2(x)))
+
+    def _fusable(self, x):
+        """Inference on the GPU: dropout inactive and nothing to differentiate."""
+        if self.training or not x.is_cuda or not isinstance(self.attention, MultiHeadConvNNAttention):
+            return False
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return False
+        return self.norm1.weight.dtype == x.dtype
+
+    def _forward_fused(self, x):
+        """The same block with its prologue and epilogues fused: LayerNorm
+        kernels, W_o with the residual add in its epilogue, fc1 with bias + GELU
+        and fc2 with bias + residual in theirs."""
+        fc1, fc2 = self.mlp[0], self.mlp[3]
+        h = ops.layernorm(x, self.norm1.weight, self.norm1.bias, self.norm1.eps)
+        z, _ = self.attention.core(h)
+        x1 = ops.linear(z, self.attention.W_o.weight, residual=x)
+        h2 = ops.layernorm(x1, self.norm2.weight, self.norm2.bias, self.norm2.eps)
+        m = ops.linear(h2, fc1.weight, fc1.bias, gelu=True)
+        return ops.linear(m, fc2.weight, fc2.bias, residual=x1)
 
 
 class ViT(nn.Module):

@@ -180,6 +180,32 @@ int cnna_core_backward(const cnna_desc* d, const void* x, int64_t ldx, const int
                        const void* conv_w1, const cnna_saved* saved, const void* dz,
                        const cnna_grads* grads, void* ws, size_t ws_bytes, void* stream);
 
+/* ---- ViT block around the operator (vit.py:247-269), inference path ----
+ * Activation codes for cnna_linear. */
+enum cnna_act { CNNA_ACT_NONE = 0, CNNA_ACT_GELU = 1 };
+
+/* nn.LayerNorm(C) over the last dimension (vit.py:247-248, applied at
+ * vit.py:262 and 267), optionally with the residual add in front of it
+ * (x + attention output, vit.py:264):  s = x + res (rounded to dtype, written
+ * to sum_out when not NULL), y = (s - mean) / sqrt(var + eps) * gamma + beta.
+ * rows x C with row strides in elements; res, sum_out, gamma, beta may be NULL
+ * (no residual / not written / 1 / 0).  C <= 1024. */
+int cnna_layernorm(int32_t dtype, int64_t rows, int32_t C, const void* x, int64_t ldx, const void* res,
+                   int64_t ldr, void* sum_out, int64_t ld_sum, const void* gamma, const void* beta,
+                   float eps, void* y, int64_t ldy, void* stream);
+
+/* nn.Linear with the epilogues of the ViT block fused:
+ *   out = act(a @ W^T + bias) + res
+ * the MLP (nn.Linear -> nn.GELU -> nn.Linear, vit.py:253-257) with its residual
+ * (vit.py:269), and W_o followed by the attention residual (vit.py:263-264).
+ * a (M, Kd) row stride lda; W (Nout, Kd) contiguous; bias (Nout) or NULL;
+ * act CNNA_ACT_*; res (M, Nout) row stride ldr or NULL; out (M, Nout) row
+ * stride ldo.  For bf16 the biased value is rounded before the activation and
+ * before the residual add, as the unfused modules round their outputs. */
+int cnna_linear(int32_t dtype, int64_t M, int32_t Nout, int32_t Kd, const void* a, int64_t lda,
+                const void* W, const void* bias, int32_t act, const void* res, int64_t ldr, void* out,
+                int64_t ldo, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
