@@ -76,6 +76,22 @@ template <> struct Mfma<float> {
   }
 };
 
+// nn.GELU() (erf form): 0.5 x (1 + erf(x / sqrt 2)) with erf from Abramowitz &
+// Stegun, Handbook of Mathematical Functions (1964), formula 7.1.26:
+//   erfc(z) = (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),  t = 1 / (1 + p z),
+// absolute error <= 1.5e-7 for z >= 0.  For x < 0 the factor 1 + erf is erfc(|z|)
+// itself (no cancellation).  About a dozen VALU operations.
+CNNA_DEV float gelu_erf(float x) {
+  const float z = fabsf(x) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, z, 1.0f));
+  float p = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+  p = __builtin_fmaf(p, t, 1.421413741f);
+  p = __builtin_fmaf(p, t, -0.284496736f);
+  p = __builtin_fmaf(p, t, 0.254829592f);
+  const float erfc = p * t * __expf(-z * z);
+  return 0.5f * x * (x >= 0.0f ? 2.0f - erfc : erfc);
+}
+
 CNNA_DEV int mfma_row(int v, int lane) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
 
 // Map a linear block id so that consecutive work items land on the same XCD
