@@ -69,8 +69,10 @@ CNNA_DEV void store4(float* p, float a, float b, float c, float d) {
   *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
 }
 
-// FAST: 16-byte loads everywhere and Kd % BK == 0 (decided by the launcher)
-template <typename T, int AMODE, int OMODE, bool FAST>
+// FAST: 16-byte loads everywhere and Kd % BK == 0 (decided by the launcher);
+// EPI: the nn.Linear extras (bias, activation, residual) of a plain output are
+// compiled in (a separate instance, so the operator's own GEMMs keep theirs lean)
+template <typename T, int AMODE, int OMODE, bool FAST, bool EPI = false>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   using M_ = Mfma<T>;
   constexpr int BK = GemmCfg<T>::BK, VEC = GemmCfg<T>::VEC;
@@ -228,7 +230,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
           const int nl = wn * 64 + j * 32 + vq * 8 + (lane >> 5) * 4;
           const f32x16_t& a = acc[i][j];
           float e[4] = {a[vq * 4], a[vq * 4 + 1], a[vq * 4 + 2], a[vq * 4 + 3]};
-          if (OMODE == GEMM_O_PLAIN && (g.bias != nullptr || g.act != GEMM_ACT_NONE)) {
+          if (EPI && (g.bias != nullptr || g.act != GEMM_ACT_NONE)) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) e[u] = lin_epi<T>(g, e[u], min(n0 + nl + u, g.Nc - 1));
           }
@@ -268,7 +270,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
       }
       if (m >= g.M || n >= g.Nc) continue;
       u32x4_t val = *reinterpret_cast<const u32x4_t*>(&Cs[ml * CP + nl]);
-      if (OMODE == GEMM_O_PLAIN && g.res != nullptr && whole) {
+      if (EPI && g.res != nullptr && whole) {
         // residual: bf16 linear output + bf16 residual, added in fp32 and rounded once
         const u32x4_t r = *reinterpret_cast<const u32x4_t*>(static_cast<const T*>(g.res) + (int64_t)m * g.ldr + n);
 #pragma unroll
@@ -293,7 +295,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
             const int h = nn / g.o_dk, c = nn - h * g.o_dk;
             static_cast<T*>(g.o[mt])[(((int64_t)b * g.o_H + h) * g.o_rows + r) * g.o_dkp + c] = v;
           } else {
-            if (g.res != nullptr)
+            if (EPI && g.res != nullptr)
               stf(&dst[u], ldf(&v) + ldf(static_cast<const T*>(g.res) + (int64_t)m * g.ldr + n + u));
             else
               dst[u] = v;
@@ -342,7 +344,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
       for (int i = 0; i < 2; ++i) {
         if (!mok[i]) continue;
         f32x16_t a = acc[i][j];
-        if (OMODE == GEMM_O_PLAIN && (g.bias != nullptr || g.act != GEMM_ACT_NONE || g.res != nullptr)) {
+        if (EPI && (g.bias != nullptr || g.act != GEMM_ACT_NONE || g.res != nullptr)) {
           const int64_t rrow = (int64_t)(m0 + wm * 64 + i * 32 + (lane & 31)) * g.ldr;
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
@@ -381,8 +383,12 @@ int launch_f(int amode, int omode, const GemmArgs& g, hipStream_t s) {
   dim3 grid(((g.Nc + BN - 1) / BN) * ((g.M + BM - 1) / BM));
   if (amode == GEMM_A_ROWS && omode == GEMM_O_HEADSPLIT)
     hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_HEADSPLIT, FAST>), grid, dim3(256), 0, s, g);
+  else if (amode == GEMM_A_ROWS && omode == GEMM_O_PLAIN && (g.bias || g.act != GEMM_ACT_NONE || g.res))
+    hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN, FAST, true>), grid, dim3(256), 0, s, g);
   else if (amode == GEMM_A_ROWS && omode == GEMM_O_PLAIN)
     hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN, FAST>), grid, dim3(256), 0, s, g);
+  else if (g.bias || g.act != GEMM_ACT_NONE || g.res)
+    return CNNA_ERR_OPTION;   // linear extras only with row-major A and a plain output
   else if (amode == GEMM_A_GATHER && omode == GEMM_O_PLAIN)
     hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_GATHER, GEMM_O_PLAIN, FAST>), grid, dim3(256), 0, s, g);
   else

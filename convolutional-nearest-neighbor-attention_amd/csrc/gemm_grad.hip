@@ -57,10 +57,28 @@ struct Operand {
   static constexpr int CE = GCfg<T>::CE, RV = GCfg<T>::RV, RB = GCfg<T>::RB;
   static constexpr int NV = 4;   // 16-byte vectors per thread per tile (both layouts)
 
-  // rows [r0, r0 + 128) of the operand, k in [k0, k0 + BK) below kend
+  // GATHER_T: neighbour index and weight of each of this thread's NV tokens
+  // for the k-step at k0, loaded one step ahead of the rows they select
+  struct Index {
+    int j[NV];
+    float w[NV];
+  };
+  static CNNA_DEV void fetch_index(Index& ix, int nrows, int r0, int k0, int kend, int tid,
+                                   const GatherArgs& ga) {
+    const int n = r0 + (tid % RB) * RV, rr = min(n, nrows - 1) / ga.din;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int k = min(k0 + (tid / RB) * 4 + i, kend - 1);
+      ix.j[i] = ga.idx[(int64_t)k * ga.K + rr];
+      ix.w[i] = ga.w[(int64_t)k * ga.K + rr];
+    }
+  }
+
+  // rows [r0, r0 + 128) of the operand, k in [k0, k0 + BK) below kend;
+  // GATHER_T with ix: the fast path takes the prefetched index and weight
   static CNNA_DEV void fetch(GPack<T> (&reg)[NV], const T* const (&base)[3], int krows, int64_t ld,
                              bool vec, int nrows, int r0, int k0, int kend, int tid,
-                             const GatherArgs& ga) {
+                             const GatherArgs& ga, const Index* ix = nullptr, float* wsave = nullptr) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       if (MODE == GG_ROWS) {
@@ -93,13 +111,17 @@ struct Operand {
         const int n = r0 + (tid % RB) * RV, k = k0 + (tid / RB) * 4 + i;
         if (k < kend && vec && n + RV <= nrows) {
           const int rr = n / ga.din, c = n - rr * ga.din;
-          const int j = ga.idx[(int64_t)k * ga.K + rr];
-          const float wv = ga.w[(int64_t)k * ga.K + rr];
+          const int j = ix ? ix->j[i] : ga.idx[(int64_t)k * ga.K + rr];
+          const float wv = ix ? ix->w[i] : ga.w[(int64_t)k * ga.K + rr];
           const T* p = base[0] + ((int64_t)(k - k % ga.N) + j) * ga.dkp + c;
-          GPack<T> v;
-          v.u = *reinterpret_cast<const u32x4_t*>(p);
+          // raw row; the weight is applied at stash time (no wait on the load here)
+          reg[i].u = *reinterpret_cast<const u32x4_t*>(p);
+          if (wsave) wsave[i] = wv;
+          else {
+            GPack<T> v = reg[i];
 #pragma unroll
-          for (int t = 0; t < RV; ++t) stf(&reg[i].e[t], wv * ldf(&v.e[t]));
+            for (int t = 0; t < RV; ++t) stf(&reg[i].e[t], wv * ldf(&v.e[t]));
+          }
         } else {
 #pragma unroll
           for (int t = 0; t < RV; ++t) {
@@ -112,8 +134,19 @@ struct Operand {
             }
             stf(&reg[i].e[t], x);
           }
+          if (wsave) wsave[i] = 1.0f;
         }
       }
+    }
+  }
+
+  // GATHER_T: scale each gathered row by its neighbour weight first
+  static CNNA_DEV void scale(GPack<T> (&reg)[NV], const float (&wsave)[NV]) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const GPack<T> v = reg[i];
+#pragma unroll
+      for (int t = 0; t < RV; ++t) stf(&reg[i].e[t], wsave[i] * ldf(&v.e[t]));
     }
   }
 
@@ -181,17 +214,26 @@ __global__ __launch_bounds__(256) void gemm_grad_kernel(GradGemmArgs g) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
+  // GATHER_T: the neighbour indices of step k + BK are loaded during step k,
+  // so the gathered rows of a step never wait on their own index loads
+  constexpr bool GI = WM == GG_GATHER_T;
+  typename OW::Index ix;
+  float wsave[OW::NV];
   if (kbeg < kend) {
     OA::fetch(ra, abase, 0, g.lda, g.avec, g.M, m0, kbeg, kend, tid, ga);
-    OW::fetch(rw, wbase, g.w_krows, g.ldw, g.bvec, g.Nc, n0, kbeg, kend, tid, ga);
+    OW::fetch(rw, wbase, g.w_krows, g.ldw, g.bvec, g.Nc, n0, kbeg, kend, tid, ga, nullptr, GI ? wsave : nullptr);
+    if (GI && kbeg + BK < kend) OW::fetch_index(ix, g.Nc, n0, kbeg + BK, kend, tid, ga);
   }
   for (int k0 = kbeg; k0 < kend; k0 += BK) {
+    if (GI) OW::scale(rw, wsave);
     OA::stash(ra, As, tid);
     OW::stash(rw, Bs, tid);
     __syncthreads();
     if (k0 + BK < kend) {
       OA::fetch(ra, abase, 0, g.lda, g.avec, g.M, m0, k0 + BK, kend, tid, ga);
-      OW::fetch(rw, wbase, g.w_krows, g.ldw, g.bvec, g.Nc, n0, k0 + BK, kend, tid, ga);
+      OW::fetch(rw, wbase, g.w_krows, g.ldw, g.bvec, g.Nc, n0, k0 + BK, kend, tid, ga, GI ? &ix : nullptr,
+                GI ? wsave : nullptr);
+      if (GI && k0 + 2 * BK < kend) OW::fetch_index(ix, g.Nc, n0, k0 + 2 * BK, kend, tid, ga);
     }
 #pragma unroll
     for (int ks = 0; ks < BK / M_::KC; ++ks) {
@@ -202,30 +244,53 @@ __global__ __launch_bounds__(256) void gemm_grad_kernel(GradGemmArgs g) {
         af[i] = M_::load(&As[lds_off<T>(wm * 64 + i * 32 + (lane & 31), kk)]);
         bfr[i] = M_::load(&Bs[lds_off<T>(wn * 64 + i * 32 + (lane & 31), kk)]);
       }
+      // transposed blocks (W as the MFMA A operand): a lane ends with 4
+      // consecutive output columns of one row, stored as one vector
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = M_::mma(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < 2; ++j) acc[i][j] = M_::mma(bfr[j], af[i], acc[i][j]);
     }
     __syncthreads();
   }
 
-  // acc[i][j][v] = out[m][n], m = m0 + wm*64 + i*32 + mfma_row(v, lane),
-  //                n = n0 + wn*64 + j*32 + lane%32 (adjacent lanes, adjacent columns)
+  // acc[i][j][v] = out[m][n], m = m0 + wm*64 + i*32 + lane%32,
+  //                n = n0 + wn*64 + j*32 + mfma_row(v, lane) (4 consecutive per v / 4)
+  const bool vec = (g.Nc % 4 == 0) && (g.part != nullptr || (g.ldo % 4 == 0 && ((uintptr_t)g.o % (4 * sizeof(T))) == 0));
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-    if (n >= g.Nc) continue;
+  for (int i = 0; i < 2; ++i) {
+    const int m = m0 + wm * 64 + i * 32 + (lane & 31);
+    if (m >= g.M) continue;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = m0 + wm * 64 + i * 32 + mfma_row(v, lane);
-        if (m >= g.M) continue;
-        if (g.part != nullptr)
-          g.part[((int64_t)split * g.M + m) * g.Nc + n] = acc[i][j][v];
-        else
-          stf(static_cast<T*>(g.o) + (int64_t)m * g.ldo + n, acc[i][j][v]);
+      for (int vq = 0; vq < 4; ++vq) {
+        const int n = n0 + wn * 64 + j * 32 + vq * 8 + (lane >> 5) * 4;
+        if (n >= g.Nc) continue;
+        const float* a4 = &acc[i][j][vq * 4];
+        if (vec && n + 4 <= g.Nc) {
+          if (g.part != nullptr) {
+            *reinterpret_cast<float4*>(&g.part[((int64_t)split * g.M + m) * g.Nc + n]) =
+                make_float4(a4[0], a4[1], a4[2], a4[3]);
+          } else {
+            T* dst = static_cast<T*>(g.o) + (int64_t)m * g.ldo + n;
+            if constexpr (sizeof(T) == 2) {
+              uint2 u;
+              u.x = f2bf2(a4[0], a4[1]);
+              u.y = f2bf2(a4[2], a4[3]);
+              *reinterpret_cast<uint2*>(dst) = u;
+            } else {
+              *reinterpret_cast<float4*>(dst) = make_float4(a4[0], a4[1], a4[2], a4[3]);
+            }
+          }
+        } else {
+          for (int u = 0; u < 4 && n + u < g.Nc; ++u) {
+            if (g.part != nullptr)
+              g.part[((int64_t)split * g.M + m) * g.Nc + n + u] = a4[u];
+            else
+              stf(static_cast<T*>(g.o) + (int64_t)m * g.ldo + n + u, a4[u]);
+          }
+        }
       }
   }
 }
