@@ -48,10 +48,10 @@ CNNA_DEV u32x4_t scale_vec(u32x4_t s, float w, float) {
 // Linear epilogue before the store: v + bias[n], then the activation.  For
 // bf16 the biased value is rounded to bf16 first, as the unfused nn.Linear ->
 // nn.GELU sequence rounds it.
-template <typename T>
+template <typename T, int EPI>
 CNNA_DEV float lin_epi(const GemmArgs& g, float v, int n) {
   if (g.bias != nullptr) v += ldf(static_cast<const T*>(g.bias) + n);
-  if (g.act == GEMM_ACT_GELU) {
+  if (EPI == 2) {
     if (sizeof(T) == 2) v = bf2f(f2bf(v));
     v = gelu_erf(v);
   }
@@ -70,10 +70,12 @@ CNNA_DEV void store4(float* p, float a, float b, float c, float d) {
 }
 
 // FAST: 16-byte loads everywhere and Kd % BK == 0 (decided by the launcher);
-// EPI: the nn.Linear extras (bias, activation, residual) of a plain output are
-// compiled in (a separate instance, so the operator's own GEMMs keep theirs lean)
-template <typename T, int AMODE, int OMODE, bool FAST, bool EPI = false>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+// EPI: the nn.Linear extras of a plain output are compiled in (0: none, 1: bias
+// and residual, 2: bias, GELU and residual), as separate instances so the
+// operator's own GEMMs keep their epilogues lean
+// (three blocks per CU: accumulators in AGPRs + VGPRs within 168 registers)
+template <typename T, int AMODE, int OMODE, bool FAST, int EPI = 0>
+__global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
   using M_ = Mfma<T>;
   constexpr int BK = GemmCfg<T>::BK, VEC = GemmCfg<T>::VEC;
   constexpr int LDS_STRIDE = BK + VEC;      // elements; rows stay 16-byte aligned
@@ -220,25 +222,54 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     // operand buffers) and written back as whole 16-byte row segments
     constexpr int CP = BN + 8;                              // staged row pitch
     T* Cs = As;                                             // 128 * 136 <= As + Bs
+    // linear extras: per column block j, this lane's 16 bias values (the same
+    // for both row blocks), 4 consecutive columns at a time
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 2; ++j) {
+      float bq[EPI ? 4 : 1][4];
+      if (EPI) {
+        const T* bp = static_cast<const T*>(g.bias);
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+        for (int vq = 0; vq < (EPI ? 4 : 1); ++vq) {
+          const int n = n0 + wn * 64 + j * 32 + vq * 8 + (lane >> 5) * 4;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) bq[vq][u] = 0.0f;
+          if (bp != nullptr) {
+            if (n + 4 <= g.Nc && ((uintptr_t)(bp + n) % 8) == 0) {
+              const uint2 b2 = *reinterpret_cast<const uint2*>(bp + n);
+              bq[vq][0] = __uint_as_float(b2.x << 16);
+              bq[vq][1] = __uint_as_float(b2.x & 0xffff0000u);
+              bq[vq][2] = __uint_as_float(b2.y << 16);
+              bq[vq][3] = __uint_as_float(b2.y & 0xffff0000u);
+            } else {
+#pragma unroll
+              for (int u = 0; u < 4; ++u) bq[vq][u] = ldf(bp + min(n + u, g.Nc - 1));
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int vq = 0; vq < 4; ++vq) {
           const int ml = wm * 64 + i * 32 + (lane & 31);
           const int nl = wn * 64 + j * 32 + vq * 8 + (lane >> 5) * 4;
           const f32x16_t& a = acc[i][j];
           float e[4] = {a[vq * 4], a[vq * 4 + 1], a[vq * 4 + 2], a[vq * 4 + 3]};
-          if (EPI && (g.bias != nullptr || g.act != GEMM_ACT_NONE)) {
+          if (EPI) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) e[u] = lin_epi<T>(g, e[u], min(n0 + nl + u, g.Nc - 1));
+            for (int u = 0; u < 4; ++u) {
+              float v = e[u] + bq[EPI ? vq : 0][u];
+              if (EPI == 2) v = gelu_erf(bf2f(f2bf(v)));   // rounded as nn.Linear's output
+              e[u] = v;
+            }
           }
           uint2 u;
           u.x = f2bf2(e[0], e[1]);
           u.y = f2bf2(e[2], e[3]);
           *reinterpret_cast<uint2*>(&Cs[ml * CP + nl]) = u;
         }
+    }
     __syncthreads();
     // thread -> fixed 8-column group nl, rows ml = (tid >> 4) + 16 * it: the
     // head-split coordinates are derived once and stepped, not divided per row
@@ -344,12 +375,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
       for (int i = 0; i < 2; ++i) {
         if (!mok[i]) continue;
         f32x16_t a = acc[i][j];
-        if (EPI && (g.bias != nullptr || g.act != GEMM_ACT_NONE || g.res != nullptr)) {
+        if (EPI) {
           const int64_t rrow = (int64_t)(m0 + wm * 64 + i * 32 + (lane & 31)) * g.ldr;
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const int n = min(nq + u, g.Nc - 1);
-            float v = lin_epi<T>(g, a[vq * 4 + u], n);
+            float v = lin_epi<T, EPI>(g, a[vq * 4 + u], n);
             if (g.res != nullptr) {
               if (sizeof(T) == 2) v = bf2f(f2bf(v));
               v += ldf(static_cast<const T*>(g.res) + rrow + n);
@@ -383,8 +414,10 @@ int launch_f(int amode, int omode, const GemmArgs& g, hipStream_t s) {
   dim3 grid(((g.Nc + BN - 1) / BN) * ((g.M + BM - 1) / BM));
   if (amode == GEMM_A_ROWS && omode == GEMM_O_HEADSPLIT)
     hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_HEADSPLIT, FAST>), grid, dim3(256), 0, s, g);
-  else if (amode == GEMM_A_ROWS && omode == GEMM_O_PLAIN && (g.bias || g.act != GEMM_ACT_NONE || g.res))
-    hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN, FAST, true>), grid, dim3(256), 0, s, g);
+  else if (amode == GEMM_A_ROWS && omode == GEMM_O_PLAIN && g.act == GEMM_ACT_GELU)
+    hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN, FAST, 2>), grid, dim3(256), 0, s, g);
+  else if (amode == GEMM_A_ROWS && omode == GEMM_O_PLAIN && (g.bias || g.res))
+    hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN, FAST, 1>), grid, dim3(256), 0, s, g);
   else if (amode == GEMM_A_ROWS && omode == GEMM_O_PLAIN)
     hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN, FAST>), grid, dim3(256), 0, s, g);
   else if (g.bias || g.act != GEMM_ACT_NONE || g.res)

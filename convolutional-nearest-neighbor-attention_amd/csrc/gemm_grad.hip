@@ -267,7 +267,7 @@ __global__ __launch_bounds__(256) void gemm_grad_kernel(GradGemmArgs g) {
       for (int vq = 0; vq < 4; ++vq) {
         const int n = n0 + wn * 64 + j * 32 + vq * 8 + (lane >> 5) * 4;
         if (n >= g.Nc) continue;
-        const float* a4 = &acc[i][j][vq * 4];
+        const float a4[4] = {acc[i][j][vq * 4], acc[i][j][vq * 4 + 1], acc[i][j][vq * 4 + 2], acc[i][j][vq * 4 + 3]};
         if (vec && n + 4 <= g.Nc) {
           if (g.part != nullptr) {
             *reinterpret_cast<float4*>(&g.part[((int64_t)split * g.M + m) * g.Nc + n]) =
