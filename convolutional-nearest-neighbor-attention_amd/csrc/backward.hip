@@ -29,40 +29,6 @@ CNNA_DEV float wave_sum(float x) {
   return x;
 }
 
-// Wave sums of KM per-lane values at once (KM = 16 or 32): each halving step
-// over lane bit b trades half of the values with lane l ^ 2^b, so KM - 1
-// exchanges plus 6 - log2(KM) full-sum steps replace KM separate wave sums.
-// Lane l ends with the sum of value slot_of(l); slot r is held by lane_of(r).
-template <int KM>
-CNNA_DEV float wave_sums(const float (&p)[KM], int lane) {
-  constexpr int LB = KM == 16 ? 4 : 5;
-  float cur[KM];
-#pragma unroll
-  for (int v = 0; v < KM; ++v) cur[v] = p[v];
-#pragma unroll
-  for (int b = 0; b < LB; ++b) {
-    const int half = KM >> (b + 1);
-    const bool hi = (lane >> b) & 1;
-#pragma unroll
-    for (int v = 0; v < half; ++v) {
-      const float send = hi ? cur[v] : cur[half + v];
-      const float keep = hi ? cur[half + v] : cur[v];
-      cur[v] = keep + __shfl_xor(send, 1 << b);
-    }
-  }
-#pragma unroll
-  for (int b = LB; b < 6; ++b) cur[0] += __shfl_xor(cur[0], 1 << b);
-  return cur[0];
-}
-template <int KM>
-CNNA_DEV int wave_sums_lane_of(int r) {   // a lane holding slot r (bit reversal over log2 KM bits)
-  constexpr int LB = KM == 16 ? 4 : 5;
-  int l = 0;
-#pragma unroll
-  for (int b = 0; b < LB; ++b) l |= ((r >> (LB - 1 - b)) & 1) << b;
-  return l;
-}
-
 // CPL consecutive channels starting at c0 of a row; zero beyond lim.
 template <typename T, int CPL> struct Row;
 template <> struct Row<uint16_t, 1> {
@@ -167,10 +133,7 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
   const bool gvec = (a.din % CPL) == 0;
   const int ntok = a.BH * a.N;
   const int nw = gridDim.x * 4;
-  // consecutive blocks on one XCD (shared L2) walk consecutive tokens, so the
-  // gathered v and q rows of a head stay L2-resident
-  const int blk = xcd_swizzle(blockIdx.x, gridDim.x);
-  for (int tok = blk * 4 + wv; tok < ntok; tok += nw) {
+  for (int tok = blockIdx.x * 4 + wv; tok < ntok; tok += nw) {
     const int bh = tok / a.N, i = tok - bh * a.N;
     const int b = bh / a.H, h = bh - b * a.H;
     const int64_t ebase = (int64_t)tok * K;
@@ -186,12 +149,10 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
     float gv[CPL];
     if (DW) load_row<T, CPL>(static_cast<const T*>(a.g) + (int64_t)tok * a.din, c0, a.din, gvec, gv);
 
-    // dw[r] = sum_c dP[c, r] * v[c, idx[r]]: per-lane partial dots of all r
-    // first (the row loads of different r overlap), then one multi-value sum
-    float part[KMAX];
+    // dw[r] = sum_c dP[c, r] * v[c, idx[r]]
+    float my_dw = 0.0f;
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) {
-      part[r] = 0.0f;
       if (r < K) {
         const int t = __builtin_amdgcn_readlane(my_j, r);
         float vv[CPL];
@@ -211,11 +172,10 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
 #pragma unroll
           for (int u = 0; u < CPL; ++u) p += dp[u] * vv[u];
         }
-        part[r] = p;
+        p = wave_sum(p);
+        if (lane == r) my_dw = p;
       }
     }
-    const float sums = wave_sums<KMAX>(part, lane);
-    const float my_dw = __shfl(sums, wave_sums_lane_of<KMAX>(lane & (KMAX - 1)));
 
     // weight backward -> dS (layers.py:342-437)
     float ds;
@@ -467,7 +427,7 @@ __global__ __launch_bounds__(256) void pull_kernel(PullArgs a) {
     }
     __syncthreads();
   }
-  const int64_t gw = (int64_t)xcd_swizzle(blockIdx.x, gridDim.x) * 4 + wv;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + wv;
   if (gw >= (int64_t)a.BH * a.nkeys) return;
   const int bh = (int)(gw / a.nkeys), key = (int)(gw - (int64_t)bh * a.nkeys);
   const int b = bh / a.H, h = bh - b * a.H;
