@@ -47,7 +47,15 @@ namespace {
 constexpr int TJ = 32;      // candidates per tile (one 32-row MFMA block)
 constexpr int NB = TJ / 32; // MFMA blocks per tile
 constexpr int TPB = 128;    // tokens per block
-constexpr int QC = 12;      // queue capacity per lane (drained when a lane passes QC - QCHK)
+// Queue capacity per lane (drained when a lane passes QC - QCHK; block-wide
+// drains at tile boundaries when any lane holds more than BTHR).  Narrow bf16
+// heads (<= 128 bytes per row) with K <= 9 leave room in LDS for 16 slots at
+// three blocks per CU, which removes most drains on short rows; otherwise 12.
+template <typename T, int NCH, bool EXACT, int KMAX>
+constexpr int queue_cap() {
+  return (EXACT && NCH * Mfma<T>::KC * (int)sizeof(T) <= 128 && KMAX <= 9) ? 16 : 12;
+}
+constexpr int QCMIN = 12;
 constexpr int QCHK = 4;     // elements between queue checks
 constexpr int NT = 256;     // threads per block
 
@@ -156,6 +164,7 @@ void select_kernel(SelArgs a) {
   T* qt = reinterpret_cast<T*>(smem);
   float* qnt = reinterpret_cast<float*>(smem + 2 * TJ * QS * sizeof(T));
   int* cdt = reinterpret_cast<int*>(qnt + 2 * TJ);
+  constexpr int QC = queue_cap<T, NCH, EXACT, KMAX>();
   // queue: key bits [QC][NT] followed by candidate indices [QC][NT]; the two
   // stores of an append share one address (ds_write2st64_b32)
   int* dflag = cdt + 2 * TJ;   // [2][4] per-wave drain requests, by tile parity
@@ -383,7 +392,7 @@ void select_kernel(SelArgs a) {
     // drain on its own mid-tile stalls the other waves at the next barrier, so
     // at every tile boundary all waves drain together when any lane of the
     // block holds more than BTHR entries (flags written before the barrier).
-    constexpr int BTHR = 6;
+    constexpr int BTHR = QC == 16 ? 10 : 6;
     auto filter_tile = [&](const f32x16_t (&acc)[NB], int buf, int j0, auto MASKED)
                            __attribute__((always_inline)) {
       const int t = j0 / TJ;
@@ -491,7 +500,11 @@ void select_kernel(SelArgs a) {
 }
 
 template <typename T, int NCH, bool EXACT, int KMAX>
-int launch_k(int euclid, int sampled, const SelArgs& a, size_t smem, dim3 grid, hipStream_t s) {
+int launch_k(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
+  constexpr int QC = queue_cap<T, NCH, EXACT, KMAX>();
+  const size_t smem = 2 * TJ * (a.dkp + SelCfg<T>::VEC) * sizeof(T) + 2 * TJ * (sizeof(float) + sizeof(int)) +
+                      8 * sizeof(int) + (size_t)QC * NT * 2 * sizeof(uint32_t) + (size_t)KMAX * TPB * sizeof(uint64_t);
+  const dim3 grid(a.BH * a.rb_per_bh);
   if (!euclid && !sampled)
     hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, false, false>), grid, dim3(NT), smem, s, a);
   else if (!euclid && sampled)
@@ -504,10 +517,10 @@ int launch_k(int euclid, int sampled, const SelArgs& a, size_t smem, dim3 grid, 
 }
 
 template <typename T, int NCH>
-int launch_n(int euclid, int sampled, const SelArgs& a, size_t smem, dim3 grid, hipStream_t s) {
-  if (a.Ksel <= 9) return launch_k<T, NCH, true, 9>(euclid, sampled, a, smem, grid, s);
-  if (a.Ksel <= 16) return launch_k<T, NCH, true, 16>(euclid, sampled, a, smem, grid, s);
-  if (a.Ksel <= 32) return launch_k<T, NCH, true, 32>(euclid, sampled, a, smem, grid, s);
+int launch_n(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
+  if (a.Ksel <= 9) return launch_k<T, NCH, true, 9>(euclid, sampled, a, s);
+  if (a.Ksel <= 16) return launch_k<T, NCH, true, 16>(euclid, sampled, a, s);
+  if (a.Ksel <= 32) return launch_k<T, NCH, true, 32>(euclid, sampled, a, s);
   return CNNA_ERR_K_RANGE;
 }
 
@@ -517,23 +530,15 @@ int launch_select_t(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
     return CNNA_ERR_SHAPE;
   if (a.Nq > 65536) return CNNA_ERR_SHAPE;
   // the queue region also stages one output array (TPB * K <= TPB * 32 values) at the end
-  static_assert(TPB * 32 <= QC * NT * 2, "output staging must fit the queue region");
-  const size_t queue = (size_t)QC * NT * 2 * sizeof(uint32_t);
-  const int nch0 = a.dkp / Mfma<T>::KC;
-  const bool exact = nch0 == SelCfg<T>::MAXCH / 4 || nch0 == SelCfg<T>::MAXCH / 2 || nch0 == SelCfg<T>::MAXCH;
-  const int kmax = !exact ? 32 : (a.Ksel <= 9 ? 9 : (a.Ksel <= 16 ? 16 : 32));
-  const size_t lists = (size_t)kmax * TPB * sizeof(uint64_t);
-  const size_t smem = 2 * TJ * (a.dkp + SelCfg<T>::VEC) * sizeof(T) + 2 * TJ * (sizeof(float) + sizeof(int)) + 8 * sizeof(int) +
-                      queue + lists;
-  dim3 grid(a.BH * a.rb_per_bh);
+  static_assert(TPB * 32 <= QCMIN * NT * 2, "output staging must fit the queue region");
   const int nch = a.dkp / Mfma<T>::KC;
   constexpr int q = SelCfg<T>::MAXCH / 4;   // head widths 64, 128, 256 (bf16) / 32, 64, 128 (f32)
-  if (nch == q) return launch_n<T, q>(euclid, sampled, a, smem, grid, s);
-  if (nch == 2 * q) return launch_n<T, 2 * q>(euclid, sampled, a, smem, grid, s);
-  if (nch == 4 * q) return launch_n<T, 4 * q>(euclid, sampled, a, smem, grid, s);
+  if (nch == q) return launch_n<T, q>(euclid, sampled, a, s);
+  if (nch == 2 * q) return launch_n<T, 2 * q>(euclid, sampled, a, s);
+  if (nch == 4 * q) return launch_n<T, 4 * q>(euclid, sampled, a, s);
   // other widths: guarded chunks, list of 32
   if (a.Ksel > 32) return CNNA_ERR_K_RANGE;
-  return launch_k<T, SelCfg<T>::MAXCH, false, 32>(euclid, sampled, a, smem, grid, s);
+  return launch_k<T, SelCfg<T>::MAXCH, false, 32>(euclid, sampled, a, s);
 }
 
 }  // namespace
