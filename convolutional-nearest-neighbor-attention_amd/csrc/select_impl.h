@@ -47,14 +47,6 @@ namespace {
 constexpr int TJ = 32;      // candidates per tile (one 32-row MFMA block)
 constexpr int NB = TJ / 32; // MFMA blocks per tile
 constexpr int TPB = 128;    // tokens per block
-// Queue capacity per lane (drained when a lane passes QC - QCHK; block-wide
-// drains at tile boundaries when any lane holds more than BTHR).  Narrow bf16
-// heads (<= 128 bytes per row) with K <= 9 leave room in LDS for 16 slots at
-// three blocks per CU, which removes most drains on short rows; otherwise 12.
-template <typename T, int NCH, bool EXACT, int KMAX>
-constexpr int queue_cap() {
-  return (EXACT && NCH * Mfma<T>::KC * (int)sizeof(T) <= 128 && KMAX <= 9) ? 16 : 12;
-}
 constexpr int QCMIN = 12;
 constexpr int QCHK = 4;     // elements between queue checks
 constexpr int NT = 256;     // threads per block
@@ -138,6 +130,20 @@ constexpr int sel_min_blocks() {
             ((!EUC && !SMP) || KFR * KMAX <= 288)) ? 2 : 1;
 }
 
+// Queue capacity per lane (drained when a lane passes QC - QCHK; block-wide
+// drains at tile boundaries when any lane holds more than QC - 6).  An entry
+// is 6 bytes (key bits, 16-bit candidate index; Nq <= 65536); the capacity is
+// the largest of 20 / 16 / 12 slots whose LDS footprint still allows the
+// instance's blocks per CU: more slots, fewer drains.
+template <typename T, int NCH, bool EXACT, int KMAX, bool EUC, bool SMP>
+constexpr int queue_cap() {
+  constexpr int VEC = SelCfg<T>::VEC;
+  constexpr int dk = NCH * Mfma<T>::KC;
+  constexpr int fixed = 2 * 32 * (dk + VEC) * (int)sizeof(T) + 2 * 32 * 8 + 32 + KMAX * 128 * 8;
+  constexpr int budget = (160 * 1024) / sel_min_blocks<NCH * (sizeof(T) == 2 ? 4 : 1), KMAX, EUC, SMP>() - 1024;
+  return !EXACT ? 12 : (fixed + 20 * 256 * 6 <= budget ? 20 : (fixed + 16 * 256 * 6 <= budget ? 16 : 12));
+}
+
 template <typename T, int NCH, bool EXACT, int KMAX, bool EUC, bool SMP>
 __global__ __launch_bounds__(NT, (sel_min_blocks<NCH * (sizeof(T) == 2 ? 4 : 1), KMAX, EUC, SMP>()))
 void select_kernel(SelArgs a) {
@@ -164,9 +170,9 @@ void select_kernel(SelArgs a) {
   T* qt = reinterpret_cast<T*>(smem);
   float* qnt = reinterpret_cast<float*>(smem + 2 * TJ * QS * sizeof(T));
   int* cdt = reinterpret_cast<int*>(qnt + 2 * TJ);
-  constexpr int QC = queue_cap<T, NCH, EXACT, KMAX>();
-  // queue: key bits [QC][NT] followed by candidate indices [QC][NT]; the two
-  // stores of an append share one address (ds_write2st64_b32)
+  constexpr int QC = queue_cap<T, NCH, EXACT, KMAX, EUC, SMP>();
+  // queue: key bits [QC][NT] (32-bit) followed by candidate indices [QC][NT]
+  // (16-bit), element woff of lane tid at qent[woff + tid] / qidx[woff + tid]
   int* dflag = cdt + 2 * TJ;   // [2][4] per-wave drain requests, by tile parity
   uint32_t* qent = reinterpret_cast<uint32_t*>(dflag + 8);
 
@@ -303,7 +309,8 @@ void select_kernel(SelArgs a) {
   // of lst), owned by the lower half-lane: only the drains and the output
   // touch it.  0 marks an empty slot.
   const int slot = wave * 32 + col;
-  uint64_t* lst = reinterpret_cast<uint64_t*>(qent + 2 * QC * NT);
+  uint16_t* qidx = reinterpret_cast<uint16_t*>(qent + QC * NT);
+  uint64_t* lst = reinterpret_cast<uint64_t*>(qent + QC * NT + QC * NT / 2);
   if (half == 0) {
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) lst[r * TPB + slot] = 0;
@@ -361,6 +368,7 @@ void select_kernel(SelArgs a) {
     // ---------------- pass 2: filter + queue
 
     uint32_t* myq = qent + tid;
+    uint16_t* myqi = qidx + tid;
     int woff = 0;   // cnt * NT: offset of this lane's next queue slot
     // both half-lanes' queues go into the token's list; only the lower half works
     auto drain = [&]() __attribute__((always_inline)) {
@@ -374,9 +382,9 @@ void select_kernel(SelArgs a) {
         const int n = cnt > cntp ? cnt : cntp;
         for (int e = 0; __any(e < n); ++e) {
           // lanes past a count insert 0, which never moves the list
-          const uint64_t x0 = (e < cnt) ? pack_entry(__uint_as_float(myq[e * NT]), myq[e * NT + QC * NT]) : 0;
+          const uint64_t x0 = (e < cnt) ? pack_entry(__uint_as_float(myq[e * NT]), myqi[e * NT]) : 0;
           const uint64_t x1 =
-              (e < cntp) ? pack_entry(__uint_as_float(myq[e * NT + 32]), myq[e * NT + 32 + QC * NT]) : 0;
+              (e < cntp) ? pack_entry(__uint_as_float(myq[e * NT + 32]), myqi[e * NT + 32]) : 0;
           list_insert<KMAX>(L2, x0);
           list_insert<KMAX>(L2, x1);
         }
@@ -392,7 +400,7 @@ void select_kernel(SelArgs a) {
     // drain on its own mid-tile stalls the other waves at the next barrier, so
     // at every tile boundary all waves drain together when any lane of the
     // block holds more than BTHR entries (flags written before the barrier).
-    constexpr int BTHR = QC == 16 ? 10 : 6;
+    constexpr int BTHR = QC - 6;
     auto filter_tile = [&](const f32x16_t (&acc)[NB], int buf, int j0, auto MASKED)
                            __attribute__((always_inline)) {
       const int t = j0 / TJ;
@@ -413,13 +421,13 @@ void select_kernel(SelArgs a) {
             // store the passers only; element steps where no lane passes skip it
             if (key >= tau) {
               myq[woff] = __float_as_uint(key);
-              myq[woff + QC * NT] = (uint32_t)(j0 + jl);
+              myqi[woff] = (uint16_t)(j0 + jl);
               woff += NT;
             }
           } else {
             // branch-free: write at the current slot, keep it only if it passed
             myq[woff] = __float_as_uint(key);
-            myq[woff + QC * NT] = (uint32_t)(j0 + jl);
+            myqi[woff] = (uint16_t)(j0 + jl);
             woff += (key >= tau) ? NT : 0;
           }
         }
@@ -501,18 +509,23 @@ void select_kernel(SelArgs a) {
 
 template <typename T, int NCH, bool EXACT, int KMAX>
 int launch_k(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
-  constexpr int QC = queue_cap<T, NCH, EXACT, KMAX>();
-  const size_t smem = 2 * TJ * (a.dkp + SelCfg<T>::VEC) * sizeof(T) + 2 * TJ * (sizeof(float) + sizeof(int)) +
-                      8 * sizeof(int) + (size_t)QC * NT * 2 * sizeof(uint32_t) + (size_t)KMAX * TPB * sizeof(uint64_t);
+  auto smem = [&](int qc) {
+    return 2 * TJ * (a.dkp + SelCfg<T>::VEC) * sizeof(T) + 2 * TJ * (sizeof(float) + sizeof(int)) + 8 * sizeof(int) +
+           (size_t)qc * NT * 6 + (size_t)KMAX * TPB * sizeof(uint64_t);
+  };
   const dim3 grid(a.BH * a.rb_per_bh);
   if (!euclid && !sampled)
-    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, false, false>), grid, dim3(NT), smem, s, a);
+    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, false, false>), grid, dim3(NT),
+                       smem(queue_cap<T, NCH, EXACT, KMAX, false, false>()), s, a);
   else if (!euclid && sampled)
-    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, false, true>), grid, dim3(NT), smem, s, a);
+    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, false, true>), grid, dim3(NT),
+                       smem(queue_cap<T, NCH, EXACT, KMAX, false, true>()), s, a);
   else if (euclid && !sampled)
-    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, true, false>), grid, dim3(NT), smem, s, a);
+    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, true, false>), grid, dim3(NT),
+                       smem(queue_cap<T, NCH, EXACT, KMAX, true, false>()), s, a);
   else
-    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, true, true>), grid, dim3(NT), smem, s, a);
+    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, true, true>), grid, dim3(NT),
+                       smem(queue_cap<T, NCH, EXACT, KMAX, true, true>()), s, a);
   return (int)hipGetLastError();
 }
 
@@ -530,7 +543,7 @@ int launch_select_t(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
     return CNNA_ERR_SHAPE;
   if (a.Nq > 65536) return CNNA_ERR_SHAPE;
   // the queue region also stages one output array (TPB * K <= TPB * 32 values) at the end
-  static_assert(TPB * 32 <= QCMIN * NT * 2, "output staging must fit the queue region");
+  static_assert(TPB * 32 * 2 <= QCMIN * NT * 3, "output staging must fit the queue region");
   const int nch = a.dkp / Mfma<T>::KC;
   constexpr int q = SelCfg<T>::MAXCH / 4;   // head widths 64, 128, 256 (bf16) / 32, 64, 128 (f32)
   if (nch == q) return launch_n<T, q>(euclid, sampled, a, s);
