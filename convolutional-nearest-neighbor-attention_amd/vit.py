@@ -47,9 +47,17 @@ class PatchEmbedding(nn.Module):
         self.flatten = nn.Flatten(start_dim=2)
 
     def forward(self, x):
-        x = self.flatten(self.linear_projection(x)).transpose(1, 2)
         if x.is_cuda and not self.training and not torch.is_grad_enabled() and self.norm.weight.dtype == x.dtype:
-            return ops.layernorm(x, self.norm.weight, self.norm.bias, self.norm.eps)
+            # inference: the stride = kernel convolution is a GEMM over the patches
+            # (one permuting copy, the MFMA GEMM with its bias, the LayerNorm kernel)
+            conv = self.linear_projection
+            B, cin, h, w = x.shape
+            p, q = conv.kernel_size
+            patches = x.view(B, cin, h // p, p, w // q, q).permute(0, 2, 4, 1, 3, 5).reshape(
+                B, (h // p) * (w // q), cin * p * q)
+            y = ops.linear(patches, conv.weight.reshape(conv.out_channels, -1), conv.bias)
+            return ops.layernorm(y, self.norm.weight, self.norm.bias, self.norm.eps)
+        x = self.flatten(self.linear_projection(x)).transpose(1, 2)
         return self.norm(x)
 
 

@@ -83,22 +83,33 @@ def _tiny_vit(dtype):
     return model
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_vit_fused_blocks_match_composable(dtype):
-    model = _tiny_vit(dtype)
-    imgs = torch.randn(8, 3, 64, 64, device=DEV).to(dtype)
+def test_vit_fused_blocks_match_composable_fp32():
+    model = _tiny_vit(torch.float32)
+    imgs = torch.randn(8, 3, 64, 64, device=DEV)
     with torch.no_grad():
-        fused = model(imgs).float()
+        fused = model(imgs)
     with torch.enable_grad():                       # parameters require grad -> composable path
         assert not model.transformer_encoder[0]._fusable(imgs.new_zeros(1, 65, 192, device=DEV))
-        plain = model(imgs).float().detach()
-    if dtype == torch.float32:
-        torch.testing.assert_close(fused, plain, rtol=1e-4, atol=1e-4)
-    else:
-        # bf16: LayerNorm / GEMM roundings differ by an ulp here and there, which can
-        # flip near-tied neighbours; compare the logits as a whole
-        rel = (fused - plain).norm() / plain.norm()
-        assert rel < 5e-2, rel.item()
+        plain = model(imgs).detach()
+    torch.testing.assert_close(fused, plain, rtol=1e-4, atol=1e-4)
+
+
+def test_vit_fused_blocks_bf16_as_accurate_as_composable():
+    # bf16: LayerNorm / GEMM roundings differ by an ulp here and there, which can
+    # flip near-tied neighbours, so both bf16 paths are measured against the
+    # float32 network with the same weights and the fused one may not be worse
+    model32 = _tiny_vit(torch.float32)
+    model16 = _tiny_vit(torch.bfloat16)
+    model16.load_state_dict({k: v.to(torch.bfloat16) for k, v in model32.state_dict().items()})
+    imgs = torch.randn(16, 3, 64, 64, device=DEV)
+    with torch.no_grad():
+        ref = model32(imgs)
+        fused = model16(imgs.to(torch.bfloat16)).float()
+    with torch.enable_grad():
+        plain = model16(imgs.to(torch.bfloat16)).float().detach()
+    err_f = ((fused - ref).norm() / ref.norm()).item()
+    err_p = ((plain - ref).norm() / ref.norm()).item()
+    assert err_f <= 1.5 * err_p + 0.02, (err_f, err_p)
 
 
 def test_vit_fused_block_is_the_one_that_runs():
@@ -110,3 +121,17 @@ def test_vit_fused_block_is_the_one_that_runs():
     model.train()
     with torch.no_grad():
         assert not blk._fusable(x)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_patch_embedding_gemm_matches_conv(dtype):
+    from vit import PatchEmbedding
+    torch.manual_seed(3)
+    pe = PatchEmbedding(192, (64, 64), (8, 8)).to(DEV).to(dtype).eval()
+    x = torch.randn(5, 3, 64, 64, device=DEV).to(dtype)
+    with torch.no_grad():
+        fused = pe(x).float()                         # GEMM + LayerNorm kernels
+    with torch.enable_grad():
+        ref = pe(x).float().detach()                  # Conv2d + nn.LayerNorm
+    tol = 1e-4 if dtype == torch.float32 else 3e-2
+    torch.testing.assert_close(fused, ref, rtol=tol, atol=tol)
