@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(HERE, "libcnna.so")
 CNNA_F32, CNNA_BF16 = 0, 1
 METRICS = {"matmul": 0, "cosine": 1, "euclidean": 2}
 CONVS = {"standard": 0, "depthwise": 1, "depthwise-separable": 2}
+MERGE_REFERENCE, MERGE_CONCAT = 0, 1
 
 ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_OPTION, ERR_K_RANGE, ERR_SEQ, ERR_WS, ERR_GROUPS = (
     -1, -2, -3, -4, -5, -6, -7, -8)
@@ -30,13 +31,13 @@ class Desc(ctypes.Structure):
 
     _fields_ = [(n, ctypes.c_int32) for n in (
         "B", "N", "C", "H", "Nq", "K", "seq_length", "dtype", "metric", "conv",
-        "softmax", "sampled", "coord")]
+        "softmax", "sampled", "coord", "merge")] + [("scale", ctypes.c_float)]
 
 
 class Saved(ctypes.Structure):
     """Mirror of ``cnna_saved``."""
 
-    _fields_ = [(n, ctypes.c_void_p) for n in ("q", "k", "v", "qn", "kn", "idx", "vals", "w")]
+    _fields_ = [(n, ctypes.c_void_p) for n in ("q", "k", "v", "qn", "kn", "idx", "vals", "w", "wmul")]
 
 
 class Grads(ctypes.Structure):
@@ -72,6 +73,8 @@ def _load():
                                 ctypes.POINTER(Grads), P, ctypes.c_size_t, P], I32),
         "cnna_layernorm": ([I32, I64, I32, P, I64, P, I64, P, I64, P, P, ctypes.c_float, P, I64, P], I32),
         "cnna_linear": ([I32, I64, I32, I32, P, I64, P, P, I32, P, I64, P, I64, P], I32),
+        "cnna_conv1d_branch_workspace": ([I32] * 6, ctypes.c_size_t),
+        "cnna_conv1d_branch": ([I32] * 6 + [P, I64, P, P, P, P, P, P, P, I64, P, ctypes.c_size_t, P], I32),
     }
     for name, (args, res) in sigs.items():
         f = getattr(lib, name)
@@ -85,7 +88,8 @@ EXPORTED = ("cnna_abi_version", "cnna_error_string", "cnna_check_desc", "cnna_he
             "cnna_project_qkv", "cnna_select", "cnna_aggregate_workspace", "cnna_aggregate",
             "cnna_output_proj", "cnna_forward_workspace", "cnna_forward",
             "cnna_output_proj_backward_workspace", "cnna_output_proj_backward",
-            "cnna_core_backward_workspace", "cnna_core_backward", "cnna_layernorm", "cnna_linear")
+            "cnna_core_backward_workspace", "cnna_core_backward", "cnna_layernorm", "cnna_linear",
+            "cnna_conv1d_branch_workspace", "cnna_conv1d_branch")
 ACT_NONE, ACT_GELU = 0, 1
 
 
@@ -119,9 +123,10 @@ def dtype_code(dt: torch.dtype) -> int:
     raise TypeError(f"cnna: unsupported dtype {dt} (float32 or bfloat16)")
 
 
-def make_desc(B, N, C, H, Nq, K, seq_length, dtype, metric, conv, softmax, sampled, coord) -> Desc:
+def make_desc(B, N, C, H, Nq, K, seq_length, dtype, metric, conv, softmax, sampled, coord,
+              merge=MERGE_REFERENCE, scale=0.0) -> Desc:
     d = Desc(B, N, C, H, Nq, K, seq_length, dtype_code(dtype), METRICS[metric], CONVS[conv],
-             int(bool(softmax)), int(bool(sampled)), int(bool(coord)))
+             int(bool(softmax)), int(bool(sampled)), int(bool(coord)), int(merge), float(scale))
     check(LIB.cnna_check_desc(ctypes.byref(d)))
     return d
 
@@ -134,10 +139,24 @@ def head_stride(d: Desc) -> int:
 # stage wrappers (each allocates its outputs with torch, launches, no sync)
 # --------------------------------------------------------------------------
 
+def _token_rows(x: torch.Tensor) -> torch.Tensor:
+    """(B, N, C) whose tokens are rows of one stride (a channel slice of a wider
+    tensor qualifies) as is, anything else as a contiguous copy."""
+    if x.stride(2) != 1 or x.stride(0) != x.shape[1] * x.stride(1):
+        return x.contiguous()
+    return x
+
+
+def _out_rows(out: torch.Tensor, B: int, N: int, C: int) -> int:
+    """Row stride of a caller-provided (B, N, C) output view."""
+    if (tuple(out.shape) != (B, N, C) or out.stride(2) != 1 or out.stride(0) != N * out.stride(1)):
+        raise ValueError("cnna: out must be (B, N, C) with unit channel stride and one token stride")
+    return out.stride(1)
+
+
 def project_qkv(d: Desc, x: torch.Tensor, cand: Optional[torch.Tensor], Wq, Wk, Wv):
     """Returns q (BH,Nq,dkp), k, v (BH,N,dkp), qn, kn (euclidean norms or None)."""
-    if x.stride(2) != 1 or x.stride(0) != x.shape[1] * x.stride(1):
-        x = x.contiguous()
+    x = _token_rows(x)
     ldx = x.stride(1)
     BH, dkp = d.B * d.H, head_stride(d)
     q = torch.empty((BH, d.Nq, dkp), dtype=x.dtype, device=x.device)
@@ -177,11 +196,14 @@ def aggregate(d: Desc, v, idx, w, w0, w1=None):
     return z
 
 
-def output_proj(d: Desc, z, Wo):
-    """out = z @ Wo^T (z already carries the reference's head-merge mixing)."""
-    out = torch.empty((d.B, d.N, d.C), dtype=z.dtype, device=z.device)
+def output_proj(d: Desc, z, Wo, out=None):
+    """out = z @ Wo^T (z already carries the reference's head-merge mixing).
+    ``out``: optional (B, N, C) view to write into (e.g. a channel slice)."""
+    if out is None:
+        out = torch.empty((d.B, d.N, d.C), dtype=z.dtype, device=z.device)
+    ldo = _out_rows(out, d.B, d.N, d.C)
     check(LIB.cnna_output_proj(ctypes.byref(d), _ptr(z.contiguous()), _ptr(Wo.contiguous()),
-                               _ptr(out), d.C, _stream()))
+                               _ptr(out), ldo, _stream()))
     return out
 
 
@@ -240,6 +262,27 @@ def linear(a, W, bias=None, gelu=False, residual=None):
     return out.view(*a.shape[:-1], Nout)
 
 
+def conv1d_branch(x, Wx, bx, conv_w, conv_b, Wo, bo, num_heads, out=None):
+    """MultiHeadConv1dAttention's forward (layers.py:452-499) through the
+    native kernels: W_x GEMM, per-head token Conv1d ('same'), the token-mixing
+    merge, W_o GEMM.  ``out``: optional (B, N, C) view to write into."""
+    x = _token_rows(x)
+    B, N, C = x.shape
+    ks = conv_w.shape[-1]
+    if out is None:
+        out = torch.empty((B, N, C), dtype=x.dtype, device=x.device)
+    ldo = _out_rows(out, B, N, C)
+    dt = dtype_code(x.dtype)
+    nws = LIB.cnna_conv1d_branch_workspace(dt, B, N, C, num_heads, ks)
+    if nws == 0:
+        raise RuntimeError("cnna: unsupported Conv1d branch shape")
+    ws = torch.empty((nws,), dtype=torch.uint8, device=x.device)
+    c = lambda t: None if t is None else _ptr(t.to(x.dtype).contiguous())
+    check(LIB.cnna_conv1d_branch(dt, B, N, C, num_heads, ks, _ptr(x), x.stride(1), c(Wx), c(bx), c(conv_w),
+                                 c(conv_b), c(Wo), c(bo), _ptr(out), ldo, _ptr(ws), nws, _stream()))
+    return out
+
+
 def output_proj_backward(d: Desc, z, Wo, dout):
     """dz = dout @ Wo, dWo = dout^T @ z."""
     dout = dout.contiguous()
@@ -256,18 +299,19 @@ def output_proj_backward(d: Desc, z, Wo, dout):
 def core_backward(d: Desc, x, cand, Wq, Wk, Wv, w0, w1, saved, dz):
     """Gradients of x, W_q, W_k, W_v and the conv weights from dz (B, N, C).
 
-    ``saved`` = (q, k, v, qn, kn, idx, vals, w) from the forward stages.
+    ``saved`` = (q, k, v, qn, kn, idx, vals, w, wmul) from the forward stages
+    (wmul: the multipliers applied to w before the aggregation, or None).
     """
-    q, k, v, qn, kn, idx, vals, w = saved
-    x = x.contiguous()
+    q, k, v, qn, kn, idx, vals, w, wmul = saved
+    x = _token_rows(x)
     dz = dz.contiguous()
     w0c = w0.to(x.dtype).contiguous()
     w1c = None if w1 is None else w1.to(x.dtype).contiguous()
-    dx = torch.empty_like(x)
+    dx = torch.empty(x.shape, dtype=x.dtype, device=x.device)
     dWq, dWk, dWv = (torch.empty(W.shape, dtype=x.dtype, device=x.device) for W in (Wq, Wk, Wv))
     dw0 = torch.empty(w0.shape, dtype=x.dtype, device=x.device)
     dw1 = None if w1 is None else torch.empty(w1.shape, dtype=x.dtype, device=x.device)
-    sv = Saved(*(None if t is None else t.data_ptr() for t in (q, k, v, qn, kn, idx, vals, w)))
+    sv = Saved(*(None if t is None else t.data_ptr() for t in (q, k, v, qn, kn, idx, vals, w, wmul)))
     gr = Grads(*(None if t is None else t.data_ptr() for t in (dx, dWq, dWk, dWv, dw0, dw1)))
     nws = LIB.cnna_core_backward_workspace(ctypes.byref(d))
     ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=x.device)
@@ -290,16 +334,20 @@ class ConvNNCore(torch.autograd.Function):
     place on the output of ``sqrt`` (layers.py:278, 291-292, 304-305), so its
     backward fails with RuntimeError for sampled euclidean; the kernels here
     can differentiate that case, and do when this flag is off.
+
+    ``wmul``: optional (B*H, N, K) fp32 multipliers applied to the neighbour
+    weights before the aggregation (dropout on attention probabilities:
+    0 or 1/(1-p)); depthwise conv only.
     """
 
     @staticmethod
-    def forward(ctx, x, Wq, Wk, Wv, w0, w1, cand, d, reference_errors=False):
+    def forward(ctx, x, Wq, Wk, Wv, w0, w1, cand, d, reference_errors=False, wmul=None):
         q, k, v, qn, kn = project_qkv(d, x, cand, Wq, Wk, Wv)
         idx, vals, w = select(d, k, q, kn, qn, cand)
-        z = aggregate(d, v, idx, w, w0, w1)
+        z = aggregate(d, v, idx, w if wmul is None else w * wmul, w0, w1)
         ctx.d = d
         ctx.reference_errors = reference_errors
-        ctx.save_for_backward(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w)
+        ctx.save_for_backward(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul)
         return z
 
     @staticmethod
@@ -310,12 +358,12 @@ class ConvNNCore(torch.autograd.Function):
                 "one of the variables needed for gradient computation has been modified by an "
                 "inplace operation: the sampled euclidean similarity is masked in place after "
                 "sqrt (layers.py:291-292, 304-305)")
-        x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w = ctx.saved_tensors
+        x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul = ctx.saved_tensors
         dx, dWq, dWk, dWv, dw0, dw1 = core_backward(ctx.d, x, cand, Wq, Wk, Wv, w0, w1,
-                                                    (q, k, v, qn, kn, idx, vals, w), dz)
+                                                    (q, k, v, qn, kn, idx, vals, w, wmul), dz)
         dw0 = dw0.to(w0.dtype)
         dw1 = None if dw1 is None else dw1.to(w1.dtype)
-        return dx, dWq, dWk, dWv, dw0, dw1, None, None, None
+        return dx, dWq, dWk, dWv, dw0, dw1, None, None, None, None
 
 
 class OutputProj(torch.autograd.Function):

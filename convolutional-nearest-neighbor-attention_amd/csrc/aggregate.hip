@@ -8,9 +8,11 @@
 //  * agg_kernel<T, VW, COPY=true>: the head merge of an already computed
 //    token-major y (standard / depthwise-separable conv paths).
 //
-// Both write either the plain token-major tensor (B*H, N, dout) or the merged
-// tensor Z (B, N, C) that enters W_o.  For H > 1 the merge mixes tokens:
-//   Z[b, t, h*dk + a] = y_bh[f] with f = a*N + t, y_bh flat token-major.
+// Both write the plain token-major tensor (B*H, N, dout) or a merged tensor
+// Z (B, N, C) (AggArgs::merged, MERGE_*).  The reference merge (H > 1, and the
+// Conv1d branch's batch_split for every H, layers.py:490-493) mixes tokens:
+//   Z[b, t, h*dk + a] = y_bh[f] with f = a*N + t, y_bh flat token-major;
+// MERGE_CONCAT places head h at columns [h*dk, (h+1)*dk) of token t.
 // A block owns TI consecutive tokens of one (b, h), i.e. the flat range
 // f in [i0*dk, (i0+TI)*dk); it stages that range in LDS as rows a of length N
 // and writes each Z row's run of consecutive columns a with adjacent lanes.
@@ -20,6 +22,10 @@
 #include "kernels.h"
 
 namespace {
+
+__host__ __device__ inline bool merge_mixes(const AggArgs& a) {
+  return (a.merged == MERGE_REFERENCE && a.H > 1) || a.merged == MERGE_MIX;
+}
 
 template <typename T, int VW> struct Vec;
 template <> struct Vec<uint16_t, 8> {
@@ -69,7 +75,7 @@ __global__ __launch_bounds__(256) void agg_kernel(AggArgs a) {
   const int i0 = (wblk - bh * a.nblk) * a.ti;
   const int ntok = min(a.ti, a.N - i0);
   const int dout = a.dout;
-  const bool stage_z = a.merged && a.H > 1;
+  const bool stage_z = merge_mixes(a);
 
   // LDS carve-up
   float* sW = reinterpret_cast<float*>(smem);                       // (K, dout) conv weights
@@ -85,7 +91,7 @@ __global__ __launch_bounds__(256) void agg_kernel(AggArgs a) {
     const T* W0 = static_cast<const T*>(a.w0);
     for (int e = tid; e < a.K * dout; e += 256) {
       const int c = e / a.K, r = e - c * a.K;
-      sW[r * dout + c] = ldf(W0 + e);
+      sW[r * dout + c] = W0 != nullptr ? ldf(W0 + e) : 1.0f;
     }
     const int64_t base = ((int64_t)bh * a.N + i0) * a.K;
     for (int e = tid; e < ntok * a.K; e += 256) {
@@ -150,8 +156,9 @@ __global__ __launch_bounds__(256) void agg_kernel(AggArgs a) {
         }
       }
     } else if (a.merged) {
-      // H == 1: Z[b, i, c] = y[b, c, i] (layers.py:248-249, 255-256)
-      Vec<T, VW>::store(static_cast<T*>(a.out) + ((int64_t)b * a.N + i) * a.C + c0, acc);
+      // reference merge with H == 1: Z[b, i, c] = y[b, c, i] (layers.py:248-249, 255-256);
+      // MERGE_CONCAT: Z[b, i, h*dk + c]
+      Vec<T, VW>::store(static_cast<T*>(a.out) + ((int64_t)b * a.N + i) * a.C + h * dout + c0, acc);
     } else {
       Vec<T, VW>::store(static_cast<T*>(a.out) + ((int64_t)bh * a.N + i) * dout + c0, acc);
     }
@@ -202,7 +209,7 @@ int launch_vw(const AggArgs& a0, hipStream_t s) {
   if (lpt > 256) return CNNA_ERR_SHAPE;
   a.lpt = lpt;
   // tokens per block: about eight Z columns per row when merging, within LDS
-  const bool stage_z = a.merged && a.H > 1;
+  const bool stage_z = merge_mixes(a);
   int ti = 64;
   if (stage_z) {
     ti = (int)cnna_round_up((size_t)((8LL * a.N + a.dout - 1) / a.dout), 16);

@@ -87,10 +87,11 @@ CNNA_DEV void store_row(T* row, int c0, int dk, const float (&o)[CPL]) {
 
 // ------------------------------------------------------------------ unmerge
 // Inverse of the head merge Z[b, t, h*dk + a] = y_bh[a*N + t] (H > 1) and of
-// the transpose Z[b, i, c] = y_b[i*dk + c] (H == 1), y_bh flat token-major.
+// the transpose Z[b, i, c] = y_b[i*dk + c] (H == 1), y_bh flat token-major;
+// concat: Z[b, t, h*dk + c] = y_bh[t*dk + c] for every H.
 template <typename T>
 __global__ __launch_bounds__(256) void unmerge_kernel(const T* dz, T* dy, int BH, int N, int dk,
-                                                      int H, int C) {
+                                                      int H, int C, int concat) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t per = (int64_t)N * dk;
   if (e >= (int64_t)BH * per) return;
@@ -98,8 +99,9 @@ __global__ __launch_bounds__(256) void unmerge_kernel(const T* dz, T* dy, int BH
   const int64_t f = e - (int64_t)bh * per;
   const int b = bh / H, h = bh - b * H;
   int64_t src;
-  if (H == 1) {
-    src = (int64_t)b * N * C + f;
+  if (H == 1 || concat) {
+    const int t = (int)(f / dk), c = (int)(f - (int64_t)t * dk);
+    src = ((int64_t)b * N + t) * C + h * dk + c;
   } else {
     const int a = (int)(f / N), t = (int)(f - (int64_t)a * N);
     src = ((int64_t)b * N + t) * C + h * dk + a;
@@ -139,12 +141,14 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
     const int64_t ebase = (int64_t)tok * K;
     const bool valid = lane < K;
     int my_j = 0;
-    float my_w = 0.0f, my_val = 0.0f;
+    float my_w = 0.0f, my_val = 0.0f, my_mul = 1.0f;
     if (valid) {
       my_j = a.idx[ebase + lane];
       my_w = a.w[ebase + lane];
       my_val = a.vals[ebase + lane];
+      if (a.wmul != nullptr) my_mul = a.wmul[ebase + lane];
     }
+    const float my_wa = my_w * my_mul;   // the weight the aggregation used
     const T* V = static_cast<const T*>(a.v) + (int64_t)bh * a.N * a.dkp;
     float gv[CPL];
     if (DW) load_row<T, CPL>(static_cast<const T*>(a.g) + (int64_t)tok * a.din, c0, a.din, gvec, gv);
@@ -159,7 +163,7 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
         load_row<T, CPL>(V + (int64_t)t * a.dkp, c0, a.dkp, true, vv);
         float p = 0.0f;
         if (DW) {
-          const float wr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), r));
+          const float wr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_wa), r));
 #pragma unroll
           for (int u = 0; u < CPL; ++u) {
             const float pr = gv[u] * vv[u];
@@ -177,6 +181,8 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
       }
     }
 
+    // through the dropout multiplier back to the weight itself
+    my_dw *= my_mul;
     // weight backward -> dS (layers.py:342-437)
     float ds;
     if (a.softmax) {
@@ -447,7 +453,7 @@ __global__ __launch_bounds__(256) void pull_kernel(PullArgs a) {
     const int e = list[x];
     const int i = e / a.K, r = e - i * a.K;
     if (a.do_v) {
-      const float we = a.w[bh * NK + e];
+      const float we = a.w[bh * NK + e] * (a.wmul != nullptr ? a.wmul[bh * NK + e] : 1.0f);
       float gg[CPL];
       if (a.std_conv) {
         load_row<T, CPL>(DP + (bh * NK + e) * a.din, c0, a.din, gvec, gg);
@@ -547,15 +553,15 @@ inline dim3 grid_for(int64_t n) { return dim3((unsigned)((n + 255) / 256)); }
 }  // namespace
 
 int launch_unmerge(int dtype, const void* dz, void* dy, int BH, int N, int dk, int H, int C,
-                   hipStream_t s) {
+                   int concat, hipStream_t s) {
   const int64_t n = (int64_t)BH * N * dk;
   if (n <= 0) return 0;
   if (dtype == CNNA_BF16)
     hipLaunchKernelGGL(unmerge_kernel<uint16_t>, grid_for(n), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(dz), static_cast<uint16_t*>(dy), BH, N, dk, H, C);
+                       static_cast<const uint16_t*>(dz), static_cast<uint16_t*>(dy), BH, N, dk, H, C, concat);
   else if (dtype == CNNA_F32)
     hipLaunchKernelGGL(unmerge_kernel<float>, grid_for(n), dim3(256), 0, s,
-                       static_cast<const float*>(dz), static_cast<float*>(dy), BH, N, dk, H, C);
+                       static_cast<const float*>(dz), static_cast<float*>(dy), BH, N, dk, H, C, concat);
   else
     return CNNA_ERR_DTYPE;
   return (int)hipGetLastError();

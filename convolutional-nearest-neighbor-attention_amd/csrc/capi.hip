@@ -44,7 +44,9 @@ int cnna_check_desc(const cnna_desc* d) {
   if (d->Nq < 0 || (!d->sampled && d->Nq != d->N)) return CNNA_ERR_SHAPE;
   if (ksel_of(d) > d->Nq) return CNNA_ERR_K_RANGE;
   if (ksel_of(d) > 32 || d->K > 32) return CNNA_ERR_K_RANGE;
-  if (d->H > 1 && d->seq_length != d->N) return CNNA_ERR_SEQ_LENGTH;
+  if (d->merge != CNNA_MERGE_REFERENCE && d->merge != CNNA_MERGE_CONCAT) return CNNA_ERR_OPTION;
+  if (d->scale != 0.0f && (d->metric != CNNA_MATMUL || !isfinite(d->scale))) return CNNA_ERR_OPTION;
+  if (d->merge == CNNA_MERGE_REFERENCE && d->H > 1 && d->seq_length != d->N) return CNNA_ERR_SEQ_LENGTH;
   const int dkp = dkp_of(d);
   if (d->dtype == CNNA_BF16 && dkp > 256) return CNNA_ERR_SHAPE;
   if (d->dtype == CNNA_F32 && dkp > 128) return CNNA_ERR_SHAPE;
@@ -138,9 +140,8 @@ int cnna_select(const cnna_desc* d, const void* k, const void* q, const float* k
   a.BH = d->B * d->H; a.N = d->N; a.Nq = d->Nq; a.dkp = dkp_of(d);
   a.K = d->K; a.Ksel = ksel_of(d);
   a.rb_per_bh = (d->N + 127) / 128;
-  const int dk = d->C / d->H;
   // matmul: S = k.q / d_k**0.5 (layers.py:324); cosine inputs are normalised
-  a.kscale = (d->metric == CNNA_MATMUL) ? (float)(1.0 / sqrt((double)dk)) : 1.0f;
+  a.kscale = (d->metric == CNNA_MATMUL) ? matmul_scale(d) : 1.0f;
   if (d->metric == CNNA_EUCLIDEAN) {
     a.mask_val = 1.1f;                         // INF (layers.py:234)
     a.mask_key = -(a.mask_val * a.mask_val);
@@ -180,7 +181,7 @@ int cnna_aggregate(const cnna_desc* d, const void* v, const int32_t* idx, const 
   a.idx = idx; a.w = w; a.BH = BH; a.N = d->N; a.K = d->K; a.dkp = dkp; a.H = d->H; a.C = d->C;
   if (d->conv == CNNA_CONV_DEPTHWISE) {
     // y = depthwise conv over the gathered neighbours, written merged
-    a.v = v; a.w0 = conv_w0; a.out = z; a.dout = dk; a.merged = 1;
+    a.v = v; a.w0 = conv_w0; a.out = z; a.dout = dk; a.merged = merge_mode(d);
     return launch_aggregate(d->dtype, a, s);
   }
   char* p = static_cast<char*>(ws);
@@ -207,7 +208,7 @@ int cnna_aggregate(const cnna_desc* d, const void* v, const int32_t* idx, const 
   } else {
     // depthwise stage (din channels) then the pointwise conv as a GEMM
     void* t1 = p;
-    a.v = v; a.w0 = conv_w0; a.out = t1; a.dout = din; a.merged = 0;
+    a.v = v; a.w0 = conv_w0; a.out = t1; a.dout = din; a.merged = MERGE_PLAIN;
     if ((st = launch_aggregate(d->dtype, a, s))) return st;
     g.Kd = din;
     g.a = t1;
@@ -218,7 +219,7 @@ int cnna_aggregate(const cnna_desc* d, const void* v, const int32_t* idx, const 
     if ((st = launch_gemm(d->dtype, GEMM_A_ROWS, GEMM_O_PLAIN, g, s))) return st;
   }
   // head merge of y into z
-  a.v = y; a.out = z; a.dout = dk; a.merged = 1; a.w0 = nullptr;
+  a.v = y; a.out = z; a.dout = dk; a.merged = merge_mode(d); a.w0 = nullptr;
   return launch_merge(d->dtype, a, s);
 }
 

@@ -152,6 +152,7 @@ int cnna_core_backward(const cnna_desc* d, const void* x, int64_t ldx, const int
   if (!gr->dx || !gr->dWq || !gr->dWk || !gr->dWv || !gr->dconv_w0) return CNNA_ERR_NULL;
   if (d->conv == CNNA_CONV_DWSEP && (!conv_w1 || !gr->dconv_w1)) return CNNA_ERR_NULL;
   if (d->sampled && !cand) return CNNA_ERR_NULL;
+  if (sv->wmul && d->conv != CNNA_CONV_DEPTHWISE) return CNNA_ERR_OPTION;
   if (ldx < d->C) return CNNA_ERR_SHAPE;
   if (ws_bytes < cnna_core_backward_workspace(d)) return CNNA_ERR_WORKSPACE;
   if (!aligned16(ws)) return CNNA_ERR_SHAPE;
@@ -163,7 +164,8 @@ int cnna_core_backward(const cnna_desc* d, const void* x, int64_t ldx, const int
   const int ntok = BH * N;
 
   // 1. inverse head merge: dy (BH, N, dk)
-  if ((st = launch_unmerge(dt, dz, p.dy, BH, N, dk, H, C, s))) return st;
+  if ((st = launch_unmerge(dt, dz, p.dy, BH, N, dk, H, C, d->merge == CNNA_MERGE_CONCAT, s)))
+    return st;
 
   // 2. conv backward down to dP / g
   const void* g_dw = nullptr;   // gradient at the depthwise-conv output (depthwise modes)
@@ -213,7 +215,8 @@ int cnna_core_backward(const cnna_desc* d, const void* x, int64_t ldx, const int
   t.BH = BH; t.N = N; t.Nq = Nq; t.K = K; t.din = din; t.dk = dk; t.dkp = dkp; t.H = H;
   t.metric = d->metric; t.softmax = d->softmax; t.sampled = d->sampled;
   t.std_conv = d->conv == CNNA_CONV_STANDARD;
-  t.scale = (float)(1.0 / sqrt((double)dk));
+  t.scale = matmul_scale(d);
+  t.wmul = sv->wmul;
   if ((st = launch_tok_bwd(dt, t, s))) return st;
   if (d->conv != CNNA_CONV_STANDARD &&
       (st = launch_w0_reduce(dt, p.w0part, tok_bwd_blocks(BH, N), din * K, gr->dconv_w0, s)))
@@ -230,7 +233,8 @@ int cnna_core_backward(const cnna_desc* d, const void* x, int64_t ldx, const int
   memset(&pa, 0, sizeof(pa));
   pa.off = p.off; pa.list = p.list; pa.nkeys = N;
   pa.do_v = 1;
-  pa.g = g_dw; pa.dP = p.dP; pa.w0 = conv_w0; pa.w = sv->w; pa.std_conv = t.std_conv;
+  pa.g = g_dw; pa.dP = p.dP; pa.w0 = conv_w0; pa.w = sv->w; pa.wmul = sv->wmul;
+  pa.std_conv = t.std_conv;
   pa.dst_v = p.dqkv; pa.ld_v = ld3; pa.off_v = offV;
   pa.coef = p.coef; pa.k = sv->k; pa.q = sv->q; pa.qn = sv->qn; pa.metric = d->metric;
   pa.BH = BH; pa.N = N; pa.K = K; pa.din = din; pa.dk = dk; pa.dkp = dkp; pa.H = H;

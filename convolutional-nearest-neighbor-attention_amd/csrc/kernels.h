@@ -102,10 +102,16 @@ struct AggArgs {
   void* out;           // merged Z (B, N, C) or plain (BH, N, dout)
   int BH, N, K, dout, dkp;
   int H, C;
-  int merged;          // 1: write Z (head merge), 0: plain token-major
+  int merged;          // MERGE_*
   int lpt, ti, nblk;   // set by the launcher
 };
-// depthwise conv over the gathered neighbours
+// Output layouts of the aggregate / merge kernels:
+//   PLAIN      token-major (BH, N, dout)
+//   REFERENCE  the ConvNN head merge (layers.py:247-259): token-mixing when H > 1, transpose when H == 1
+//   CONCAT     heads side by side, Z[b, t, h*dout + c] (MultiHeadKvtAttention, layers.py:683)
+//   MIX        the token-mixing merge for every H (MultiHeadConv1dAttention, layers.py:490-497)
+enum { MERGE_PLAIN = 0, MERGE_REFERENCE = 1, MERGE_CONCAT = 2, MERGE_MIX = 3 };
+// conv over the gathered neighbours; w0 == NULL: unit weights (plain weighted sum)
 int launch_aggregate(int dtype, const AggArgs& a, hipStream_t s);
 // head merge of a token-major y into Z
 int launch_merge(int dtype, const AggArgs& a, hipStream_t s);
@@ -163,9 +169,10 @@ struct ReduceArgs {
 };
 int launch_splitk_reduce(int dtype, const ReduceArgs& r, hipStream_t s);
 
-// Inverse head merge: dy (BH, N, dk) token-major from dZ (B, N, C).
+// Inverse head merge: dy (BH, N, dk) token-major from dZ (B, N, C), the
+// reference merge or (concat) heads side by side.
 int launch_unmerge(int dtype, const void* dz, void* dy, int BH, int N, int dk, int H, int C,
-                   hipStream_t s);
+                   int concat, hipStream_t s);
 
 // Per token: neighbour-weight gradient, softmax / weight backward, similarity
 // gradient coefficients and the key gradient; depthwise-weight partial sums.
@@ -179,6 +186,7 @@ struct TokBwdArgs {
   const int32_t* idx;   // (BH, N, K)
   const float* vals;    // (BH, N, K)
   const float* w;       // (BH, N, K)
+  const float* wmul;    // (BH, N, K) multipliers applied to w before the aggregation, or NULL
   const int32_t* inv;   // sampled: token -> candidate column (or >= Nq)
   const void* w0;       // depthwise weight (din, 1, K)
   float* coef;          // out: (BH, N, K) similarity-gradient coefficient
@@ -229,6 +237,7 @@ struct PullArgs {
   const void* dP;      // standard: (BH*N*K, din)
   const void* w0;      // depthwise weight (din, 1, K)
   const float* w;      // (BH, N, K)
+  const float* wmul;   // (BH, N, K) or NULL, as in TokBwdArgs
   int std_conv;
   void* dst_v;
   int64_t ld_v;
@@ -252,3 +261,19 @@ int launch_gather_rows(int dtype, const void* x, int64_t ldx, const int32_t* can
 int launch_scatter_rows(int dtype, const void* dxs, const int32_t* cand, void* dx, int B, int N,
                         int Nq, int C, hipStream_t s);
 int launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t s);
+
+// ================================================================ branches
+// Conv1d(dk, dk, ks, stride 1, padding 'same') along the tokens of each head
+// of u (B, N, H*dk) (MultiHeadConv1dAttention, layers.py:495-497):
+//   y[b*H + h][t][o] = bias[o] + sum_{c, r} w[o][c][r] * u[b][t + r - padl][h*dk + c]
+// (zero outside [0, N)), y token-major (B*H, N, dk).
+struct Conv1dArgs {
+  const void* u;
+  int64_t ldu;
+  const void* w;      // (dk, dk, ks)
+  const void* bias;   // (dk) or NULL
+  void* y;
+  int B, N, H, dk, ks, padl;
+  int tt;             // set by the launcher: tokens per block
+};
+int launch_conv1d_tokens(int dtype, const Conv1dArgs& a, hipStream_t s);

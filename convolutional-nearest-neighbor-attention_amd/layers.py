@@ -14,6 +14,8 @@ ties break by the lowest candidate index.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 import torch.nn as nn
 
@@ -129,3 +131,261 @@ class MultiHeadConvNNAttention(nn.Module):
         # dropout on the conv output (layers.py:316); elementwise, so applying it
         # after the head merge is the same operation on permuted elements
         return self.dropout(z), d
+
+
+def _inference(module: nn.Module, x: torch.Tensor) -> bool:
+    """Nothing to differentiate: the native inference kernels may run."""
+    if not x.is_cuda:
+        return False
+    if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in module.parameters())):
+        return False
+    return True
+
+
+class MultiHeadAttention(nn.Module):
+    """Softmax multi-head attention (layers.py:88-130): the sibling branch of
+    ``MultiHeadBranchingAttention`` and the ViT's ``layer="Attention"``.
+
+    Not a ConvNN path: it runs through PyTorch.  The score / softmax / value
+    products are evaluated in float32 (bfloat16 inputs are widened), so no
+    batched bfloat16 product takes a transposed operand.
+    """
+
+    def __init__(self, d_hidden, num_heads, attention_dropout):
+        super().__init__()
+        assert d_hidden % num_heads == 0, "d_hidden must be divisible by num_heads"
+        self.d_hidden = d_hidden
+        self.num_heads = num_heads
+        self.d_k = d_hidden // num_heads
+        self.dropout = nn.Dropout(attention_dropout)
+        self.W_q = nn.Linear(d_hidden, d_hidden, bias=False)
+        self.W_k = nn.Linear(d_hidden, d_hidden, bias=False)
+        self.W_v = nn.Linear(d_hidden, d_hidden, bias=False)
+        self.W_o = nn.Linear(d_hidden, d_hidden, bias=False)
+
+    def _heads(self, t):
+        B, N, _ = t.shape
+        return t.view(B, N, self.num_heads, self.d_k).transpose(1, 2).float().contiguous()
+
+    def forward(self, x, mask=None):
+        B, N, _ = x.shape
+        q, k, v = self._heads(self.W_q(x)), self._heads(self.W_k(x)), self._heads(self.W_v(x))
+        scores = torch.matmul(q, k.transpose(-2, -1).contiguous()) / math.sqrt(self.d_k)
+        if mask is not None:
+            scores = scores.masked_fill(mask == 0, -1e9)                 # layers.py:111-112
+        probs = self.dropout(torch.softmax(scores, dim=-1))
+        o = torch.matmul(probs, v).to(x.dtype)
+        return self.W_o(o.transpose(1, 2).reshape(B, N, self.d_hidden))
+
+
+class MultiHeadConv1dAttention(nn.Module):
+    """Per-head token Conv1d (layers.py:452-499): W_x, Conv1d(d_k, d_k,
+    kernel_size, stride 1, padding 'same') shared by the heads, the reference's
+    token-mixing reshape back to (B, N, d_hidden), W_o.
+
+    Inference runs the native path (``cnna_conv1d_branch``: MFMA GEMMs for W_x
+    and W_o with their biases, a LDS-tiled token convolution, the merge
+    kernel); with gradients required it runs the same arithmetic as PyTorch
+    modules so autograd applies.
+    """
+
+    def __init__(self, d_hidden, num_heads, kernel_size):
+        super().__init__()
+        assert d_hidden % num_heads == 0, "d_hidden must be divisible by num_heads"
+        self.d_hidden = d_hidden
+        self.num_heads = num_heads
+        self.d_k = d_hidden // num_heads
+        self.kernel_size = kernel_size
+        self.stride = 1
+        self.W_x = nn.Linear(d_hidden, d_hidden)
+        self.W_o = nn.Linear(d_hidden, d_hidden)
+        self.in_channels = d_hidden // num_heads
+        self.out_channels = d_hidden // num_heads
+        self.conv = nn.Conv1d(self.in_channels, self.out_channels, kernel_size=self.kernel_size,
+                              stride=self.stride, padding="same")
+
+    def forward(self, x, out=None):
+        if _inference(self, x) and self.W_x.weight.dtype == x.dtype:
+            return ops.conv1d_branch(x, self.W_x.weight, self.W_x.bias, self.conv.weight, self.conv.bias,
+                                     self.W_o.weight, self.W_o.bias, self.num_heads, out=out)
+        y = self._forward_modules(x)
+        if out is not None:
+            out.copy_(y)
+            return out
+        return y
+
+    def _forward_modules(self, x):
+        B, N, _ = x.shape
+        H, dk = self.num_heads, self.d_k
+        u = self.W_x(x).view(B, N, H, dk).permute(0, 2, 3, 1).reshape(B * H, dk, N)  # layers.py:476-487
+        y = self.conv(u)                                                              # (B*H, d_k, N)
+        # layers.py:483-497: the token-major conv output of each head, read as
+        # (d_k, N) and transposed, z[b, t, h*d_k + a] = y_tok[b*H + h].flat[a*N + t]
+        z = y.transpose(1, 2).reshape(B, H, dk, N).transpose(2, 3).transpose(1, 2).reshape(B, N, H * dk)
+        return self.W_o(z)
+
+
+class _Branching(nn.Module):
+    """Shared forward of the two branching layers (layers.py:590-600, 644-652)."""
+
+    def _both(self, x, second):
+        d1 = self.d_hidden_convnn
+        if not (_inference(self, x) and not self.training and
+                self.pointwise_linear.weight.dtype == x.dtype):
+            x1 = self.convnn(x[:, :, :d1])
+            x2 = second(x[:, :, d1:])
+            return self.pointwise_linear(torch.cat((x1, x2), dim=2))
+        # inference: each branch writes its channel slice of one (B, N, C)
+        # tensor (no concatenation copy), the ConvNN branch straight from the
+        # strided input slice; then the pointwise linear with its bias
+        B, N, C = x.shape
+        cat = torch.empty((B, N, C), dtype=x.dtype, device=x.device)
+        z, d = self.convnn.core(x[:, :, :d1])
+        ops.output_proj(d, z, self.convnn.W_o.weight, out=cat[:, :, :d1])
+        if isinstance(second, MultiHeadConv1dAttention):
+            second(x[:, :, d1:], out=cat[:, :, d1:])
+        else:
+            cat[:, :, d1:] = second(x[:, :, d1:])
+        return ops.linear(cat, self.pointwise_linear.weight, self.pointwise_linear.bias)
+
+
+class MultiHeadBranchingConv(_Branching):
+    """ConvNN on the first ``int(branch_ratio * d_hidden)`` channels, a
+    ``MultiHeadConv1dAttention`` on the rest, concatenated and mixed by a
+    pointwise linear (layers.py:502-600).  Same constructor, attribute and
+    parameter names as the reference."""
+
+    def __init__(self, d_hidden, num_heads, attention_dropout, kernel_size, K, sampling_type,
+                 num_samples, sample_padding, magnitude_type, seq_length=197,
+                 coordinate_encoding=False, convolution_type='depthwise', softmax_topk_val=True,
+                 branch_ratio=0.5):
+        super().__init__()
+        self.d_hidden = d_hidden
+        self.num_heads = num_heads
+        self.attention_dropout = attention_dropout
+        self.kernel_size = kernel_size
+        self.K = K
+        self.sampling_type = sampling_type
+        self.num_samples = int(num_samples)
+        self.sample_padding = int(sample_padding) if sampling_type == 'spatial' else 0
+        self.magnitude_type = magnitude_type
+        self.seq_length = seq_length
+        self.coordinate_encoding = coordinate_encoding
+        self.branch_ratio = branch_ratio
+        self.d_hidden_convnn = int(self.branch_ratio * d_hidden)
+        self.d_hidden_conv1d = d_hidden - self.d_hidden_convnn
+        if self.branch_ratio != 0:
+            self.convnn = MultiHeadConvNNAttention(
+                d_hidden=self.d_hidden_convnn, num_heads=num_heads, attention_dropout=attention_dropout,
+                K=K, sampling_type=sampling_type, num_samples=num_samples, sample_padding=sample_padding,
+                magnitude_type=magnitude_type, seq_length=seq_length,
+                coordinate_encoding=coordinate_encoding, convolution_type=convolution_type,
+                softmax_topk_val=softmax_topk_val)
+        if self.branch_ratio != 1:
+            self.conv1d = MultiHeadConv1dAttention(d_hidden=self.d_hidden_conv1d, num_heads=num_heads,
+                                                   kernel_size=kernel_size)
+        self.pointwise_linear = nn.Linear(d_hidden, d_hidden)
+
+    def forward(self, x):
+        if self.branch_ratio == 0:
+            return self.conv1d(x)
+        if self.branch_ratio == 1:
+            return self.convnn(x)
+        return self._both(x, self.conv1d)
+
+
+class MultiHeadBranchingAttention(_Branching):
+    """ConvNN on the first ``int(branch_ratio * d_hidden)`` channels, softmax
+    ``MultiHeadAttention`` on the rest, concatenated and mixed by a pointwise
+    linear (layers.py:602-652).  As in the reference, ``branch_ratio`` 0 calls
+    the ConvNN branch and 1 the attention branch, neither of which exists in
+    that case (AttributeError, layers.py:645-648)."""
+
+    def __init__(self, d_hidden, num_heads, attention_dropout, K, sampling_type, num_samples,
+                 sample_padding, magnitude_type, seq_length=197, coordinate_encoding=False,
+                 convolution_type='depthwise', softmax_topk_val=True, branch_ratio=0.5):
+        super().__init__()
+        self.d_hidden = d_hidden
+        self.num_heads = num_heads
+        self.attention_dropout = attention_dropout
+        self.K = K
+        self.sampling_type = sampling_type
+        self.num_samples = int(num_samples)
+        self.sample_padding = int(sample_padding) if sampling_type == 'spatial' else 0
+        self.magnitude_type = magnitude_type
+        self.seq_length = seq_length
+        self.coordinate_encoding = coordinate_encoding
+        self.branch_ratio = branch_ratio
+        self.d_hidden_convnn = int(self.branch_ratio * d_hidden)
+        self.d_hidden_attention = d_hidden - self.d_hidden_convnn
+        if self.branch_ratio != 0:
+            self.convnn = MultiHeadConvNNAttention(
+                d_hidden=self.d_hidden_convnn, num_heads=num_heads, attention_dropout=attention_dropout,
+                K=K, sampling_type=sampling_type, num_samples=num_samples, sample_padding=sample_padding,
+                magnitude_type=magnitude_type, seq_length=seq_length,
+                coordinate_encoding=coordinate_encoding, convolution_type=convolution_type,
+                softmax_topk_val=softmax_topk_val)
+        if self.branch_ratio != 1:
+            self.attention = MultiHeadAttention(d_hidden=self.d_hidden_attention, num_heads=num_heads,
+                                                attention_dropout=attention_dropout)
+        self.pointwise_linear = nn.Linear(d_hidden, d_hidden)
+
+    def forward(self, x):
+        if self.branch_ratio == 0:
+            return self.convnn(x)
+        if self.branch_ratio == 1:
+            return self.attention(x)
+        return self._both(x, self.attention)
+
+
+class MultiHeadKvtAttention(nn.Module):
+    """Top-k sparse softmax attention (layers.py:654-686) on the streaming
+    top-k kernel instead of a dense (B, H, N, N) score matrix and scatter mask.
+
+    Each query keeps the ``topk`` keys with the largest q . k * scale (ties:
+    lowest key index), softmax over them, weighted sum of their values, heads
+    side by side, ``proj``.  That is the operator's own select -> aggregate
+    path with the roles of the projections assigned as
+    ``W_k := qkv.weight[:C]`` (rows that choose) and ``W_q := qkv.weight[C:2C]``
+    (candidates), unit depthwise weights, softmax weights and the concatenated
+    head layout; forward and backward both run natively.  ``attn_drop``
+    applies to the kept probabilities (the dropped entries of the reference's
+    dense row are zero already).  Native limits: ``topk`` <= 32 and no
+    ``qkv_bias`` (NotImplementedError otherwise).
+    """
+
+    def __init__(self, dim, num_heads=8, qkv_bias=False, qk_scale=None, attn_drop=0., proj_drop=0.,
+                 topk=100):
+        super().__init__()
+        self.num_heads = num_heads
+        head_dim = dim // num_heads
+        self.scale = qk_scale or head_dim ** -0.5
+        self.qkv = nn.Linear(dim, dim * 3, bias=qkv_bias)
+        self.attn_drop = nn.Dropout(attn_drop)
+        self.proj = nn.Linear(dim, dim, bias=False)
+        self.proj_drop = nn.Dropout(proj_drop)
+        self.topk = topk
+
+    def forward(self, x):
+        if not x.is_cuda:
+            raise RuntimeError("MultiHeadKvtAttention (cnna) runs on ROCm device tensors only")
+        if self.qkv.bias is not None:
+            raise NotImplementedError("cnna: MultiHeadKvtAttention with qkv_bias")
+        B, N, C = x.shape
+        H = self.num_heads
+        if self.topk > N:
+            raise RuntimeError("selected index k out of range")                # torch.topk
+        if self.topk > 32:
+            raise NotImplementedError("cnna: MultiHeadKvtAttention supports topk <= 32")
+        if self.qkv.weight.dtype != x.dtype:
+            raise RuntimeError(f"mat1 and mat2 must have the same dtype, but got {x.dtype} and "
+                               f"{self.qkv.weight.dtype}")
+        d = ops.make_desc(B, N, C, H, N, self.topk, N, x.dtype, "matmul", "depthwise", True, False, False,
+                          merge=ops.MERGE_CONCAT, scale=self.scale)
+        W = self.qkv.weight
+        ones = torch.ones((C // H, 1, self.topk), dtype=x.dtype, device=x.device)
+        wmul = None
+        if self.training and self.attn_drop.p > 0:
+            wmul = self.attn_drop(torch.ones((B * H, N, self.topk), dtype=torch.float32, device=x.device))
+        z = ops.ConvNNCore.apply(x, W[C:2 * C], W[:C], W[2 * C:], ones, None, None, d, False, wmul)
+        return self.proj_drop(ops.OutputProj.apply(z, self.proj.weight, d))

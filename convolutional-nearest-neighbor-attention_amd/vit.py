@@ -2,14 +2,18 @@
 
 Restates the parts of the reference ViT (vit.py:22-270) that the ConvNN-ViT
 configuration uses: patch embedding (Conv2d + LayerNorm), class token and
-sinusoidal positional encoding, pre-norm transformer blocks whose attention is
-``MultiHeadConvNNAttention`` (vit.py:190), GELU MLP and the CLS classifier.
-Module and parameter names follow the reference so state dicts carry over.
-Only ``layer="ConvNNAttention"`` is built here; the other attention families
-of the reference are outside this operator's scope and raise ValueError.
+sinusoidal positional encoding, pre-norm transformer blocks, GELU MLP and the
+CLS classifier.  Module and parameter names follow the reference so state
+dicts carry over.  The block's attention (vit.py:186-203) is one of
+``ConvNNAttention`` (the operator), ``BranchConv`` / ``BranchAttention`` (the
+operator on a channel slice beside a Conv1d or softmax-attention branch),
+``KvtAttention`` (top-k attention on the operator's select kernel) or
+``Attention``; the reference's Local / Neighborhood / Sparse attention
+families are outside this operator's scope and raise ValueError.
 
 In inference (eval mode, no gradients) each block runs with its prologue and
-epilogues fused: LayerNorm kernels, W_o + residual, fc1 + bias + GELU and
+epilogues fused: LayerNorm kernels, W_o + residual (ConvNN attention) or the
+residual add inside the second LayerNorm (other layers), fc1 + bias + GELU and
 fc2 + bias + residual in the GEMM epilogues (cnna_layernorm, cnna_linear).
 Training and autograd use the composable modules.
 """
@@ -22,7 +26,8 @@ import torch
 import torch.nn as nn
 
 import cnna_ops as ops
-from layers import MultiHeadConvNNAttention
+from layers import (MultiHeadAttention, MultiHeadBranchingAttention, MultiHeadBranchingConv,
+                    MultiHeadConvNNAttention, MultiHeadKvtAttention)
 
 
 def vit_tiny_args(**overrides) -> SimpleNamespace:
@@ -31,7 +36,7 @@ def vit_tiny_args(**overrides) -> SimpleNamespace:
              num_heads=3, d_hidden=192, d_mlp=768, dropout=0.1, attention_dropout=0.1,
              num_classes=10, K=9, sampling_type="all", num_samples=-1, sample_padding=0,
              magnitude_type="matmul", coordinate_encoding=False, convolution_type="depthwise",
-             softmax_topk_val=False)
+             softmax_topk_val=False, kernel_size=9, branch_ratio=0.5)
     a.update(overrides)
     return SimpleNamespace(**a)
 
@@ -84,14 +89,28 @@ class TransformerEncoder(nn.Module):
 
     def __init__(self, args, d_hidden, d_mlp, num_heads, dropout, attention_dropout):
         super().__init__()
-        if args.layer != "ConvNNAttention":
-            raise ValueError(f"layer {args.layer!r} is not built here; only 'ConvNNAttention'")
-        # vit.py:190 passes no seq_length (default 197)
-        self.attention = MultiHeadConvNNAttention(
-            d_hidden, num_heads, attention_dropout, K=args.K, sampling_type=args.sampling_type,
-            num_samples=args.num_samples, sample_padding=args.sample_padding,
-            magnitude_type=args.magnitude_type, coordinate_encoding=args.coordinate_encoding,
-            convolution_type=args.convolution_type, softmax_topk_val=args.softmax_topk_val)
+        # vit.py:147-203; no seq_length is passed (default 197)
+        convnn = dict(K=args.K, sampling_type=args.sampling_type, num_samples=args.num_samples,
+                      sample_padding=args.sample_padding, magnitude_type=args.magnitude_type,
+                      coordinate_encoding=args.coordinate_encoding,
+                      convolution_type=args.convolution_type, softmax_topk_val=args.softmax_topk_val)
+        if args.layer == "Attention":
+            self.attention = MultiHeadAttention(d_hidden, num_heads, attention_dropout)
+        elif args.layer == "ConvNNAttention":
+            self.attention = MultiHeadConvNNAttention(d_hidden, num_heads, attention_dropout, **convnn)
+        elif args.layer == "BranchConv":
+            self.attention = MultiHeadBranchingConv(d_hidden, num_heads, attention_dropout,
+                                                    kernel_size=args.kernel_size,
+                                                    branch_ratio=args.branch_ratio, **convnn)
+        elif args.layer == "BranchAttention":
+            self.attention = MultiHeadBranchingAttention(d_hidden, num_heads, attention_dropout,
+                                                         branch_ratio=args.branch_ratio, **convnn)
+        elif args.layer == "KvtAttention":
+            self.attention = MultiHeadKvtAttention(dim=d_hidden, num_heads=num_heads,
+                                                   attn_drop=attention_dropout, topk=args.K)
+        else:
+            raise ValueError(f"layer {args.layer!r} is not built here; one of 'Attention', "
+                             "'ConvNNAttention', 'BranchConv', 'BranchAttention', 'KvtAttention'")
         self.norm1 = nn.LayerNorm(d_hidden)
         self.norm2 = nn.LayerNorm(d_hidden)
         self.dropout1 = nn.Dropout(dropout)
@@ -107,7 +126,7 @@ class TransformerEncoder(nn.Module):
 
     def _fusable(self, x):
         """Inference on the GPU: dropout inactive and nothing to differentiate."""
-        if self.training or not x.is_cuda or not isinstance(self.attention, MultiHeadConvNNAttention):
+        if self.training or not x.is_cuda:
             return False
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
             return False
@@ -119,9 +138,14 @@ class TransformerEncoder(nn.Module):
         and fc2 with bias + residual in theirs."""
         fc1, fc2 = self.mlp[0], self.mlp[3]
         h = ops.layernorm(x, self.norm1.weight, self.norm1.bias, self.norm1.eps)
-        z, _ = self.attention.core(h)
-        x1 = ops.linear(z, self.attention.W_o.weight, residual=x)
-        h2 = ops.layernorm(x1, self.norm2.weight, self.norm2.bias, self.norm2.eps)
+        if isinstance(self.attention, MultiHeadConvNNAttention):
+            z, _ = self.attention.core(h)
+            x1 = ops.linear(z, self.attention.W_o.weight, residual=x)
+            h2 = ops.layernorm(x1, self.norm2.weight, self.norm2.bias, self.norm2.eps)
+        else:
+            a = self.attention(h)
+            h2, x1 = ops.layernorm(a, self.norm2.weight, self.norm2.bias, self.norm2.eps, residual=x,
+                                   want_sum=True)
         m = ops.linear(h2, fc1.weight, fc1.bias, gelu=True)
         return ops.linear(m, fc2.weight, fc2.bias, residual=x1)
 

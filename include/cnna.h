@@ -28,13 +28,19 @@
 extern "C" {
 #endif
 
-#define CNNA_ABI_VERSION 1
+#define CNNA_ABI_VERSION 2
 
 enum cnna_dtype { CNNA_F32 = 0, CNNA_BF16 = 1 };
 /* magnitude_type (layers.py:167-168, 323-340) */
 enum cnna_metric { CNNA_MATMUL = 0, CNNA_COSINE = 1, CNNA_EUCLIDEAN = 2 };
 /* convolution_type (layers.py:186-228) */
 enum cnna_conv { CNNA_CONV_STANDARD = 0, CNNA_CONV_DEPTHWISE = 1, CNNA_CONV_DWSEP = 2 };
+/* Head layout of the aggregated tensor z:
+ *   REFERENCE  the operator's own merge (layers.py:247-259, 316-317)
+ *   CONCAT     heads side by side, z[b, t, h*d_k + c] = y[b*H + h][t][c]: the
+ *              (attn @ v).transpose(1, 2).reshape(B, N, C) of
+ *              MultiHeadKvtAttention (layers.py:681) */
+enum cnna_merge { CNNA_MERGE_REFERENCE = 0, CNNA_MERGE_CONCAT = 1 };
 
 enum cnna_status {
   CNNA_OK = 0,
@@ -64,7 +70,18 @@ typedef struct cnna_desc {
   int32_t softmax;      /* softmax_topk_val */
   int32_t sampled;      /* 1 for 'random' / 'spatial' (layers.py:283-307) */
   int32_t coord;        /* coordinate_encoding (layers.py:269-270, 439-450) */
+  int32_t merge;        /* enum cnna_merge, 0 = the operator's own */
+  float scale;          /* matmul similarity scale; 0 = 1/sqrt(d_k) (layers.py:324) */
 } cnna_desc;
+
+/* MultiHeadKvtAttention (layers.py:654-686) is this operator with
+ *   metric MATMUL, conv DEPTHWISE with unit weights (d_k, 1, K) of ones,
+ *   softmax 1, sampled 0, K = topk, merge CONCAT, scale = its self.scale,
+ *   Wq := qkv.weight[C:2C] (its keys are the candidates, layers.py:672),
+ *   Wk := qkv.weight[0:C]  (its queries are the rows that choose),
+ *   Wv := qkv.weight[2C:3C], Wo := proj.weight:
+ * softmax over the topk largest q_i . k_j * scale of each row equals its
+ * dense row with the rest masked to -inf (layers.py:674-679). */
 
 int cnna_abi_version(void);
 const char* cnna_error_string(int code);
@@ -145,6 +162,10 @@ typedef struct cnna_saved {
   const int32_t* idx;
   const float* vals;
   const float* w;
+  /* per-entry multipliers (B*H, N, K) the forward applied to w before the
+   * aggregation (dropout on the attention probabilities: 0 or 1/(1-p),
+   * layers.py:680), or NULL; depthwise conv only */
+  const float* wmul;
 } cnna_saved;
 
 /* Gradients written by cnna_core_backward, dtype of the descriptor.
@@ -205,6 +226,24 @@ int cnna_layernorm(int32_t dtype, int64_t rows, int32_t C, const void* x, int64_
 int cnna_linear(int32_t dtype, int64_t M, int32_t Nout, int32_t Kd, const void* a, int64_t lda,
                 const void* W, const void* bias, int32_t act, const void* res, int64_t ldr, void* out,
                 int64_t ldo, void* stream);
+
+/* ---- branching callers (layers.py:502-652) ----
+ * MultiHeadConv1dAttention (layers.py:452-499), the Conv1d branch of
+ * MultiHeadBranchingConv, inference path:
+ *   u = x @ Wx^T + bx;  per head, Conv1d(d_k, d_k, ks, stride 1, padding
+ *   'same', weights conv_w (d_k, d_k, ks), bias conv_b) along the tokens;
+ *   the token-mixing reshape of layers.py:483-497, z[b, t, h*d_k + a] =
+ *   y[b*H + h][f] over the flat token-major conv output, f = a*N + t, for
+ *   every H;  out = z @ Wo^T + bo.
+ * x (B, N, C) row stride ldx; out row stride ldo (a channel slice of a wider
+ * tensor: the concatenation of layers.py:596-597 without a copy).  bx,
+ * conv_b, bo may be NULL.  ws: cnna_conv1d_branch_workspace bytes. */
+size_t cnna_conv1d_branch_workspace(int32_t dtype, int32_t B, int32_t N, int32_t C, int32_t H,
+                                    int32_t ks);
+int cnna_conv1d_branch(int32_t dtype, int32_t B, int32_t N, int32_t C, int32_t H, int32_t ks,
+                       const void* x, int64_t ldx, const void* Wx, const void* bx,
+                       const void* conv_w, const void* conv_b, const void* Wo, const void* bo,
+                       void* out, int64_t ldo, void* ws, size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -523,3 +523,80 @@ def flops(cfg: Config, B: int, N: int) -> dict:
     else:
         cv = 2 * B * N * C * (K + dk)
     return {"proj": proj, "sim": sim, "conv": cv, "total": proj + sim + cv}
+
+
+# ---------------------------------------------------------------------------
+# Callers of the operator (layers.py:452-686).  Pinning, in tests/test_oracle.py:
+#   conv1d_branch   == an element-by-element loop (padding placement, merge);
+#   mha             == a per-row softmax loop;
+#   kvt             == a per-row python sort + softmax loop; == full softmax
+#                      attention at topk == N; == the ConvNN restatement above
+#                      with H == 1 and the projections assigned as in
+#                      MultiHeadKvtAttention's docstring;
+#   branching_*     == the concatenation of the two branches by construction
+#                      (each branch pinned on its own).
+# ---------------------------------------------------------------------------
+
+def conv1d_branch(x: torch.Tensor, Wx, bx, conv_w, conv_b, Wo, bo, H: int) -> torch.Tensor:
+    """MultiHeadConv1dAttention.forward (layers.py:495-499).
+
+    W_x, split_head + batch_combine to (B*H, d_k, N), Conv1d with padding
+    'same' ((ks-1)//2 zeros in front, the rest behind), then permute +
+    batch_split + combine_heads: the token-major conv output of each head read
+    as (d_k, N) and transposed, which mixes tokens for every H
+    (``z[b, t, h*d_k + a] = y_tok[b*H + h].flat[a*N + t]``), then W_o.
+    """
+    B, N, C = x.shape
+    dk = C // H
+    u = F.linear(x, Wx, bx)
+    u = u.view(B, N, H, dk).transpose(1, 2).permute(0, 1, 3, 2).contiguous().view(-1, dk, N)
+    y = F.conv1d(u, conv_w, conv_b, stride=1, padding="same")            # (B*H, d_k, N)
+    y = y.permute(0, 2, 1).reshape(B, -1, dk, N).permute(0, 1, 3, 2).contiguous()
+    z = y.transpose(1, 2).contiguous().view(B, N, C)
+    return F.linear(z, Wo, bo)
+
+
+def mha(x: torch.Tensor, Wq, Wk, Wv, Wo, H: int, mask=None) -> torch.Tensor:
+    """MultiHeadAttention.forward in eval mode (layers.py:106-130)."""
+    B, N, C = x.shape
+    dk = C // H
+    sh = lambda t: t.view(B, N, H, dk).transpose(1, 2)
+    q, k, v = sh(F.linear(x, Wq)), sh(F.linear(x, Wk)), sh(F.linear(x, Wv))
+    s = torch.matmul(q, k.transpose(-2, -1).contiguous()) / math.sqrt(dk)
+    if mask is not None:
+        s = s.masked_fill(mask == 0, -1e9)
+    o = torch.matmul(torch.softmax(s, dim=-1), v.contiguous())
+    return F.linear(o.transpose(1, 2).contiguous().view(B, N, C), Wo)
+
+
+def kvt(x: torch.Tensor, Wqkv, Wproj, H: int, topk: int, scale: float, wmul=None,
+        bqkv=None) -> torch.Tensor:
+    """MultiHeadKvtAttention.forward (layers.py:668-686), eval mode.
+
+    attn = q k^T * scale; keep the ``topk`` largest of each row (ties: lowest
+    key index, see ``stable_topk``), -inf elsewhere; softmax; @ v; heads side
+    by side; proj.  ``wmul`` (B*H, N, topk): multipliers on the kept
+    probabilities in rank order (attention dropout with a given mask).
+    """
+    B, N, C = x.shape
+    dk = C // H
+    qkv = F.linear(x, Wqkv, bqkv).reshape(B, N, 3, H, dk).permute(2, 0, 3, 1, 4)
+    q, k, v = qkv[0], qkv[1], qkv[2]
+    attn = torch.matmul(q, k.transpose(-2, -1).contiguous()) * scale
+    vals, idx = stable_topk(attn, topk, largest=True)
+    p = torch.softmax(vals, dim=-1)                                  # == masked dense softmax
+    if wmul is not None:
+        p = p * wmul.view(B, H, N, topk).to(p.dtype)
+    vg = torch.gather(v.unsqueeze(2).expand(B, H, N, N, dk), 3,
+                      idx.unsqueeze(-1).expand(B, H, N, topk, dk))   # (B, H, N, topk, dk)
+    o = (p.unsqueeze(-1) * vg).sum(3)
+    return F.linear(o.transpose(1, 2).reshape(B, N, C), Wproj)
+
+
+def branching_conv(x: torch.Tensor, convnn_fn, conv1d_fn, Wp, bp, d1: int) -> torch.Tensor:
+    """MultiHeadBranchingConv / MultiHeadBranchingAttention forward with both
+    branches (layers.py:590-600, 644-652): branch 1 on channels [0, d1),
+    branch 2 on the rest, concatenated, pointwise linear with bias."""
+    x1 = convnn_fn(x[:, :, :d1])
+    x2 = conv1d_fn(x[:, :, d1:])
+    return F.linear(torch.cat((x1, x2), dim=2), Wp, bp)

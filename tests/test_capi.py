@@ -30,12 +30,12 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert ops.LIB.cnna_abi_version() == 1
+    assert ops.LIB.cnna_abi_version() == 2
 
 
 def desc(**kw):
     base = dict(B=2, N=16, C=12, H=3, Nq=16, K=4, seq_length=16, dtype=ops.CNNA_F32, metric=0, conv=1,
-                softmax=1, sampled=0, coord=0)
+                softmax=1, sampled=0, coord=0, merge=0, scale=0.0)
     base.update(kw)
     return ops.Desc(*[base[f] for f, _ in ops.Desc._fields_])
 
@@ -58,11 +58,20 @@ def test_check_desc_ok():
     (dict(coord=1), ops.ERR_GROUPS),                   # depthwise + coordinate encoding
     (dict(K=17), ops.ERR_K_RANGE),                     # K > candidates
     (dict(sampled=1, Nq=4, K=6), ops.ERR_K_RANGE),     # K-1 > num_samples
+    (dict(merge=2), ops.ERR_OPTION),                   # unknown head layout
+    (dict(metric=1, scale=0.5), ops.ERR_OPTION),       # a scale only for matmul
+    (dict(scale=float("inf")), ops.ERR_OPTION),
     (dict(seq_length=197), ops.ERR_SEQ),               # H > 1 and seq_length != N
     (dict(K=0), ops.ERR_K_RANGE),
 ])
 def test_check_desc_errors(kw, code):
     assert status(**kw) == code
+
+
+def test_concat_merge_ignores_seq_length():
+    # KVT's head layout has no reshape by seq_length
+    assert status(seq_length=5) == ops.ERR_SEQ
+    assert status(seq_length=5, merge=1, scale=0.25) == 0
 
 
 def test_h1_ignores_seq_length():

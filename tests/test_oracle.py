@@ -233,3 +233,135 @@ def test_gradcheck_oracle_f64():
     p = O.init_params(cfg, seed=5, dtype=torch.float64)
     x = torch.randn(B, N, C, dtype=torch.float64, requires_grad=True)
     assert torch.autograd.gradcheck(lambda t: O.forward(t, p, cfg, mode="exact"), (x,))
+
+
+# ---------------------------------------------------------------- callers
+def _rand(*shape, seed=0, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=torch.float64) * scale
+
+
+@pytest.mark.parametrize("H,ks", [(1, 3), (2, 3), (2, 4), (3, 1), (1, 6)])
+def test_conv1d_branch_elementwise_loop(H, ks):
+    """'same' padding puts (ks-1)//2 zeros in front; the merge mixes tokens
+    for every H: z[b, t, h*dk + a] = y_tok[b*H + h].flat[a*N + t]."""
+    B, N, dk = 2, 7, 2
+    C = H * dk
+    x = _rand(B, N, C, seed=1)
+    Wx, bx = _rand(C, C, seed=2), _rand(C, seed=3)
+    cw, cb = _rand(dk, dk, ks, seed=4), _rand(dk, seed=5)
+    Wo, bo = _rand(C, C, seed=6), _rand(C, seed=7)
+    got = O.conv1d_branch(x, Wx, bx, cw, cb, Wo, bo, H)
+    u = x @ Wx.T + bx
+    pl = (ks - 1) // 2
+    ytok = torch.zeros(B * H, N, dk, dtype=torch.float64)
+    for b in range(B):
+        for h in range(H):
+            for t in range(N):
+                for o in range(dk):
+                    s = float(cb[o])
+                    for r in range(ks):
+                        tt = t + r - pl
+                        if 0 <= tt < N:
+                            for c in range(dk):
+                                s += float(cw[o, c, r]) * float(u[b, tt, h * dk + c])
+                    ytok[b * H + h, t, o] = s
+    z = torch.empty(B, N, C, dtype=torch.float64)
+    for b in range(B):
+        for h in range(H):
+            flat = ytok[b * H + h].reshape(-1)
+            for t in range(N):
+                for a in range(dk):
+                    z[b, t, h * dk + a] = flat[a * N + t]
+    torch.testing.assert_close(got, z @ Wo.T + bo, rtol=1e-12, atol=1e-12)
+
+
+def test_mha_rowwise_softmax_loop():
+    B, N, H, dk = 2, 5, 2, 3
+    C = H * dk
+    x = _rand(B, N, C, seed=8)
+    Ws = [_rand(C, C, seed=9 + i, scale=0.5) for i in range(4)]
+    mask = (torch.rand(B, 1, N, N, generator=torch.Generator().manual_seed(0)) > 0.3).long()
+    mask[..., 0] = 1
+    got = O.mha(x, *Ws, H, mask=mask)
+    q, k, v = (x @ W.T for W in Ws[:3])
+    o = torch.empty(B, N, C, dtype=torch.float64)
+    for b in range(B):
+        for h in range(H):
+            sl = slice(h * dk, (h + 1) * dk)
+            for i in range(N):
+                s = [(float(q[b, i, sl] @ k[b, j, sl]) / math.sqrt(dk)) if mask[b, 0, i, j] else -1e9
+                     for j in range(N)]
+                m = max(s)
+                e = [math.exp(t - m) for t in s]
+                o[b, i, sl] = sum(e[j] / sum(e) * v[b, j, sl] for j in range(N))
+    torch.testing.assert_close(got, o @ Ws[3].T, rtol=1e-12, atol=1e-12)
+
+
+def _kvt_loop(x, Wqkv, Wproj, H, topk, scale, wmul=None):
+    B, N, C = x.shape
+    dk = C // H
+    qkv = x @ Wqkv.T
+    q, k, v = qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:]
+    o = torch.empty(B, N, C, dtype=torch.float64)
+    for b in range(B):
+        for h in range(H):
+            sl = slice(h * dk, (h + 1) * dk)
+            for i in range(N):
+                s = [float(q[b, i, sl] @ k[b, j, sl]) * scale for j in range(N)]
+                keep = sorted(range(N), key=lambda j: (-s[j], j))[:topk]
+                m = max(s[j] for j in keep)
+                e = [math.exp(s[j] - m) for j in keep]
+                p = [t / sum(e) for t in e]
+                if wmul is not None:
+                    p = [p[r] * float(wmul[b * H + h, i, r]) for r in range(topk)]
+                o[b, i, sl] = sum(p[r] * v[b, keep[r], sl] for r in range(topk))
+    return o @ Wproj.T
+
+
+@pytest.mark.parametrize("H,topk", [(1, 3), (2, 1), (3, 4)])
+def test_kvt_rowwise_loop(H, topk):
+    B, N, dk = 2, 6, 2
+    C = H * dk
+    x = _rand(B, N, C, seed=20)
+    Wqkv, Wp = _rand(3 * C, C, seed=21), _rand(C, C, seed=22)
+    wmul = (torch.rand(B * H, N, topk, generator=torch.Generator().manual_seed(1)) > 0.25).double() / 0.75
+    for wm in (None, wmul):
+        got = O.kvt(x, Wqkv, Wp, H, topk, 0.37, wmul=wm)
+        torch.testing.assert_close(got, _kvt_loop(x, Wqkv, Wp, H, topk, 0.37, wm), rtol=1e-12, atol=1e-12)
+
+
+def test_kvt_with_all_keys_is_softmax_attention():
+    B, N, H, dk = 2, 9, 3, 4
+    C = H * dk
+    x = _rand(B, N, C, seed=30)
+    Wqkv, Wp = _rand(3 * C, C, seed=31, scale=0.3), _rand(C, C, seed=32)
+    got = O.kvt(x, Wqkv, Wp, H, N, dk ** -0.5)
+    qkv = (x @ Wqkv.T).reshape(B, N, 3, H, dk).permute(2, 0, 3, 1, 4)
+    o = F.scaled_dot_product_attention(qkv[0], qkv[1], qkv[2])
+    torch.testing.assert_close(got, o.transpose(1, 2).reshape(B, N, C) @ Wp.T, rtol=1e-10, atol=1e-10)
+
+
+def test_kvt_is_the_operator_with_concat_heads_at_h1():
+    """With one head the operator's merge is the concatenation, so KVT equals
+    the ConvNN restatement with W_k := q rows, W_q := k rows, unit depthwise
+    weights, softmax weights and K = topk."""
+    B, N, C, topk = 2, 11, 5, 4
+    x = _rand(B, N, C, seed=40)
+    Wqkv, Wp = _rand(3 * C, C, seed=41), _rand(C, C, seed=42)
+    cfg = O.Config(d_hidden=C, num_heads=1, K=topk, magnitude_type="matmul",
+                   convolution_type="depthwise", softmax_topk_val=True, seq_length=N)
+    p = O.Params(Wqkv[C:2 * C], Wqkv[:C], Wqkv[2 * C:], Wp, torch.ones(C, 1, topk, dtype=torch.float64))
+    ref = O.forward(x, p, cfg)
+    torch.testing.assert_close(O.kvt(x, Wqkv, Wp, 1, topk, C ** -0.5), ref, rtol=1e-12, atol=1e-12)
+
+
+def test_branching_is_concat_of_branches():
+    B, N, C, d1 = 2, 4, 6, 2
+    x = _rand(B, N, C, seed=50)
+    Wp, bp = _rand(C, C, seed=51), _rand(C, seed=52)
+    f1 = lambda t: t * 2.0
+    f2 = lambda t: t - 1.0
+    got = O.branching_conv(x, f1, f2, Wp, bp, d1)
+    want = torch.cat((x[..., :d1] * 2.0, x[..., d1:] - 1.0), -1) @ Wp.T + bp
+    torch.testing.assert_close(got, want)
