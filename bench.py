@@ -43,7 +43,12 @@ CONFIGS = {
     "c5": (8, 4096, 768, 3, 16, torch.bfloat16, "matmul", "standard", "all", -1, 3),
     # c2: the whole ViT-Tiny (12 blocks, N = 197) in run_vit; the layer shape is c2layer
     "c2": (128, 197, 192, 3, 9, torch.bfloat16, "matmul", "depthwise", "all", -1, 0),
+    # callers at the ViT-Tiny block shape (run_callers): KVT top-k attention
+    # (topk = K) and the branching Conv1d layer (ConvNN on half the channels)
+    "kvt": (128, 197, 192, 3, 9, torch.bfloat16, "matmul", "depthwise", "all", -1, 0),
+    "branch": (128, 197, 192, 3, 9, torch.bfloat16, "matmul", "depthwise", "all", -1, 0),
 }
+CALLERS = {"kvt", "branch"}
 TRAIN = {"c5"}
 
 
@@ -256,6 +261,134 @@ def run_vit(args):
     print(json.dumps(rec), flush=True)
 
 
+def kvt_dense(x, Wqkv, Wproj, H, topk, scale):
+    """The reference's dense KVT forward (layers.py:668-686) as plain torch ops
+    on the GPU: full (B, H, N, N) scores, torch.topk, a dense 0/1 mask filled by
+    scatter_, -inf fill, softmax over N, dense probabilities @ v.  Operands of
+    the batched products are made contiguous first."""
+    B, N, C = x.shape
+    qkv = torch.nn.functional.linear(x, Wqkv).reshape(B, N, 3, H, C // H).permute(2, 0, 3, 1, 4)
+    q, k, v = qkv[0].contiguous(), qkv[1].transpose(-2, -1).contiguous(), qkv[2].contiguous()
+    attn = torch.matmul(q, k) * scale
+    mask = torch.zeros(B, H, N, N, device=x.device)
+    index = torch.topk(attn, k=topk, dim=-1, largest=True)[1]
+    mask.scatter_(-1, index, 1.0)
+    attn = torch.where(mask > 0, attn, torch.full_like(attn, float("-inf"))).softmax(dim=-1)
+    o = torch.matmul(attn, v).transpose(1, 2).reshape(B, N, C)
+    return torch.nn.functional.linear(o, Wproj)
+
+
+def run_callers(args):
+    """kvt / branch: one forward of the caller layer at the ViT-Tiny block
+    shape (B=128, N=197, C=192, H=3, K = topk = 9, bf16), inference path."""
+    import cnna_ops as ops
+    from layers import MultiHeadBranchingConv, MultiHeadKvtAttention
+
+    B, N, C, H, K, dtype, metric, conv, sampling, ns, seed = CONFIGS[args.config]
+    torch.manual_seed(seed)
+    if args.config == "kvt":
+        m = MultiHeadKvtAttention(C, num_heads=H, attn_drop=0.0, topk=K)
+        C1 = C
+    else:
+        m = MultiHeadBranchingConv(C, H, 0.0, kernel_size=9, K=K, sampling_type="all", num_samples=-1,
+                                   sample_padding=0, magnitude_type=metric, seq_length=N,
+                                   convolution_type=conv, softmax_topk_val=False, branch_ratio=0.5)
+        C1 = m.d_hidden_convnn
+    m = m.to("cuda").to(dtype).eval()
+    x = torch.randn(B, N, C, device="cuda").to(dtype)
+    calibration_copy("cuda")
+
+    def timed(fn):
+        with torch.no_grad():
+            for _ in range(args.warmup):
+                fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                fn()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e3 / args.steps
+
+    ms = timed(lambda: m(x))
+    ref_ms = None
+    if args.config == "kvt":
+        ref_ms = timed(lambda: kvt_dense(x, m.qkv.weight, m.proj.weight, H, K, m.scale))
+    # dominant stage: the select kernel at the operator's shape, HIP events on the launch stream
+    dk = C1 // H
+    if args.config == "kvt":
+        d = ops.make_desc(B, N, C, H, N, K, N, dtype, "matmul", "depthwise", True, False, False,
+                          merge=ops.MERGE_CONCAT, scale=m.scale)
+        W = m.qkv.weight
+        Wq, Wk, Wv = W[C:2 * C], W[:C], W[2 * C:]
+    else:
+        d = ops.make_desc(B, N, C1, H, N, K, N, dtype, metric, conv, False, False, False)
+        cv = m.convnn
+        Wq, Wk, Wv = cv.W_q.weight, cv.W_k.weight, cv.W_v.weight
+    ts = []
+    with torch.no_grad():
+        q, k, v, qn, kn = ops.project_qkv(d, x[:, :, :C1], None, Wq, Wk, Wv)
+        for it in range(args.warmup + args.steps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            ops.select(d, k, q, kn, qn, None)
+            e1.record()
+            if it >= args.warmup:
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1))
+    t_sel = sorted(ts)[len(ts) // 2] / 1e3
+    f_sim = 2 * B * N * N * C1
+    achieved = f_sim / t_sel / 1e12
+    cpu = None
+    if not args.no_cpu:
+        from oracle import cnna_oracle as O
+        ncores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(ncores)
+        bs = max(1, min(args.cpu_sample_batch, B))
+        xc = x[:bs].float().cpu()
+        if args.config == "kvt":
+            Wc, Pc = m.qkv.weight.float().cpu(), m.proj.weight.float().cpu()
+            fn = lambda: O.kvt(xc, Wc, Pc, H, K, m.scale)
+        else:
+            mc = __import__("copy").deepcopy(m).float().cpu()
+            cv = mc.convnn
+            cfg = O.Config(d_hidden=C1, num_heads=H, K=K, magnitude_type=metric, seq_length=N,
+                           convolution_type=conv, softmax_topk_val=False)
+            p = O.Params(cv.W_q.weight, cv.W_k.weight, cv.W_v.weight, cv.W_o.weight, cv.conv.weight)
+            c1 = mc.conv1d
+            fn = lambda: O.branching_conv(
+                xc, lambda t: O.forward(t, p, cfg),
+                lambda t: O.conv1d_branch(t, c1.W_x.weight, c1.W_x.bias, c1.conv.weight, c1.conv.bias,
+                                          c1.W_o.weight, c1.W_o.bias, H),
+                mc.pointwise_linear.weight, mc.pointwise_linear.bias, C1)
+        with torch.no_grad():
+            fn()
+            reps, t_cpu = 0, 0.0
+            while reps < 3 or (t_cpu < 10.0 and reps < 20):
+                c0 = time.perf_counter()
+                fn()
+                t_cpu += time.perf_counter() - c0
+                reps += 1
+        cpu = {"value": round(bs * N * reps / t_cpu, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+               "kind": "port", "sample": f"{reps} forwards of {bs} of {B} sequences (N={N}) in f32, "
+                                         "oracle restatement", "affinity_cores": ncores}
+    name = {"kvt": "KVT top-k attention forward tokens/s (N=197, C=192, H=3, topk=9, bf16)",
+            "branch": "BranchConv layer forward tokens/s (N=197, C=192, ratio 0.5, K=9, ks=9, bf16)"}
+    rec = {
+        "metric": name[args.config], "value": round(B * N / (ms / 1e3), 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: x ~ N(0,1), random-init weights (seeded)",
+        "config": {"workload": f"{args.config}: caller layer forward at the ViT-Tiny block shape",
+                   "B": B, "N": N, "C": C, "H": H, "K": K},
+        "roofline": {"kernel": "select", "bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+        "reference_gpu_ms": None if ref_ms is None else round(ref_ms, 4),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def main():
     args = parse()
     if args.summarize_pmc:
@@ -267,6 +400,9 @@ def main():
         sys.exit(2)
     if args.config == "c2":
         run_vit(args)
+        return
+    if args.config in CALLERS:
+        run_callers(args)
         return
     import cnna_ops as ops
     from layers import MultiHeadConvNNAttention

@@ -19,7 +19,7 @@ namespace {
 
 bool conv1d_shape_ok(int32_t dtype, int32_t B, int32_t N, int32_t C, int32_t H, int32_t ks) {
   (void)dtype;
-  return B > 0 && N > 0 && C > 0 && H > 0 && C % H == 0 && ks > 0 && ks <= 64 &&
+  return B > 0 && N > 0 && C > 0 && H > 0 && C % H == 0 && ks > 0 && ks <= 33 &&
          (int64_t)B * N * C <= INT32_MAX;
 }
 
@@ -31,7 +31,8 @@ size_t cnna_conv1d_branch_workspace(int32_t dtype, int32_t B, int32_t N, int32_t
                                     int32_t ks) {
   const int es = elem_size(dtype);
   if (!es || !conv1d_shape_ok(dtype, B, N, C, H, ks)) return 0;
-  return 3 * cnna_round_up((size_t)B * N * C * es, 256);   // u, y, z
+  return 3 * cnna_round_up((size_t)B * N * C * es, 256) +   // u, y, z
+         cnna_round_up(conv1d_wprep_bytes(C / H, ks), 256);  // conv weights, fp32 [c][o][taps]
 }
 
 int cnna_conv1d_branch(int32_t dtype, int32_t B, int32_t N, int32_t C, int32_t H, int32_t ks,
@@ -50,6 +51,8 @@ int cnna_conv1d_branch(int32_t dtype, int32_t B, int32_t N, int32_t C, int32_t H
   void* u = cv.take((size_t)B * N * C * es);
   void* y = cv.take((size_t)B * N * C * es);
   void* z = cv.take((size_t)B * N * C * es);
+  const size_t wpb = conv1d_wprep_bytes(dk, ks);
+  float* wprep = static_cast<float*>(cv.take(wpb));
   int st;
   if ((st = cnna_linear(dtype, (int64_t)B * N, C, C, x, ldx, Wx, bx, CNNA_ACT_NONE, nullptr, 0, u, C,
                         stream)))
@@ -59,6 +62,7 @@ int cnna_conv1d_branch(int32_t dtype, int32_t B, int32_t N, int32_t C, int32_t H
   c.u = u; c.ldu = C; c.w = conv_w; c.bias = conv_b; c.y = y;
   c.B = B; c.N = N; c.H = H; c.dk = dk; c.ks = ks;
   c.padl = (ks - 1) / 2;                 // torch 'same': the odd extra zero goes behind
+  c.wprep = wprep; c.wprep_bytes = wpb;
   if ((st = launch_conv1d_tokens(dtype, c, s))) return st;
   AggArgs a;
   memset(&a, 0, sizeof(a));

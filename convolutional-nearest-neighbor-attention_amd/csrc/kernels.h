@@ -274,6 +274,13 @@ struct Conv1dArgs {
   const void* bias;   // (dk) or NULL
   void* y;
   int B, N, H, dk, ks, padl;
+  float* wprep;       // scratch for the weights as fp32 [c][o][taps], or NULL
+  size_t wprep_bytes;
   int tt;             // set by the launcher: tokens per block
 };
+// bytes of Conv1dArgs::wprep that let the weights stage from LDS
+inline size_t conv1d_wprep_bytes(int dk, int ks) {
+  const int ksm = ks == 1 ? 1 : ks <= 3 ? 3 : ks <= 5 ? 5 : ks <= 9 ? 9 : ks <= 17 ? 17 : 33;
+  return (size_t)dk * dk * ksm * 4;
+}
 int launch_conv1d_tokens(int dtype, const Conv1dArgs& a, hipStream_t s);

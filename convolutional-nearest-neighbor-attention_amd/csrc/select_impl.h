@@ -191,6 +191,9 @@ void select_kernel(SelArgs a) {
   const int ntiles = (a.Nq + TJ - 1) / TJ;
   const int vpr = dkp / VEC;  // 16-byte vectors per candidate row
   constexpr int NPF = (TJ * (NCH * Mfma<T>::KC / VEC) + NT - 1) / NT;
+  // every thread's NPF vectors lie inside the tile (narrow heads have fewer
+  // vectors per tile than threads: the extra threads must not store)
+  constexpr bool FULLV = EXACT && (TJ * (NCH * Mfma<T>::KC / VEC)) % NT == 0;
 
   // ---- tile staging: unconditional loads of clamped rows (rows >= Nq are
   // masked when keys are formed), so no load sits behind a branch
@@ -228,7 +231,7 @@ void select_kernel(SelArgs a) {
     for (int i = 0; i < NPF; ++i) {
       const int e = tid + i * NT;
       const int r = e / vpr, cv = e - r * vpr;
-      if (EXACT || r < TJ) *reinterpret_cast<u32x4_t*>(dst + r * QS + cv * VEC) = pf[i];
+      if (FULLV || r < TJ) *reinterpret_cast<u32x4_t*>(dst + r * QS + cv * VEC) = pf[i];
     }
     if (tid < TJ) {
       if (EUC) qnt[buf * TJ + tid] = pfn;
@@ -545,7 +548,8 @@ int launch_select_t(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
   // the queue region also stages one output array (TPB * K <= TPB * 32 values) at the end
   static_assert(TPB * 32 * 2 <= QCMIN * NT * 3, "output staging must fit the queue region");
   const int nch = a.dkp / Mfma<T>::KC;
-  constexpr int q = SelCfg<T>::MAXCH / 4;   // head widths 64, 128, 256 (bf16) / 32, 64, 128 (f32)
+  constexpr int q = SelCfg<T>::MAXCH / 4;   // head widths 32, 64, 128, 256 (bf16) / 16 .. 128 (f32)
+  if (nch == q / 2) return launch_n<T, q / 2>(euclid, sampled, a, s);
   if (nch == q) return launch_n<T, q>(euclid, sampled, a, s);
   if (nch == 2 * q) return launch_n<T, 2 * q>(euclid, sampled, a, s);
   if (nch == 4 * q) return launch_n<T, 4 * q>(euclid, sampled, a, s);

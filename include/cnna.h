@@ -237,7 +237,7 @@ int cnna_linear(int32_t dtype, int64_t M, int32_t Nout, int32_t Kd, const void* 
  *   every H;  out = z @ Wo^T + bo.
  * x (B, N, C) row stride ldx; out row stride ldo (a channel slice of a wider
  * tensor: the concatenation of layers.py:596-597 without a copy).  bx,
- * conv_b, bo may be NULL.  ws: cnna_conv1d_branch_workspace bytes. */
+ * conv_b, bo may be NULL; ks <= 33.  ws: cnna_conv1d_branch_workspace bytes. */
 size_t cnna_conv1d_branch_workspace(int32_t dtype, int32_t B, int32_t N, int32_t C, int32_t H,
                                     int32_t ks);
 int cnna_conv1d_branch(int32_t dtype, int32_t B, int32_t N, int32_t C, int32_t H, int32_t ks,
