@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes
 import math
 import os
-from typing import Optional
+from typing import List, Optional, Tuple
 
 import torch
 
@@ -380,3 +380,201 @@ class OutputProj(torch.autograd.Function):
         z, Wo = ctx.saved_tensors
         dz, dWo = output_proj_backward(ctx.d, z, Wo, dout)
         return dz, dWo, None
+
+
+# --------------------------------------------------------------------------
+# torch.library operators: the same C-ABI calls as custom ops with fake
+# (shape-only) kernels, registered autograd and FLOP formulas, so that
+# torch.compile traces the layer without graph breaks and
+# torch.utils.flop_counter.FlopCounterMode counts it.  The eager path keeps
+# the autograd.Function classes above (lower Python dispatch cost); the
+# layers switch to these ops while compiling or under a dispatch mode.
+# --------------------------------------------------------------------------
+
+DESC_FIELDS = ("B", "N", "C", "H", "Nq", "K", "seq_length", "dtype", "metric", "conv", "softmax",
+               "sampled", "coord", "merge")
+
+
+def desc_list(d: Desc) -> list:
+    return [int(getattr(d, f)) for f in DESC_FIELDS]
+
+
+def desc_values(B, N, C, H, Nq, K, seq_length, dtype, metric, conv, softmax, sampled, coord,
+                merge=MERGE_REFERENCE):
+    """The descriptor as plain ints (no library call: traceable)."""
+    return [B, N, C, H, Nq, K, seq_length, dtype_code(dtype), METRICS[metric], CONVS[conv],
+            int(bool(softmax)), int(bool(sampled)), int(bool(coord)), int(merge)]
+
+
+def _desc_of(dl, scale) -> Desc:
+    d = Desc(*dl, float(scale))
+    check(LIB.cnna_check_desc(ctypes.byref(d)))
+    return d
+
+
+def _dkp(dl) -> int:
+    din = dl[2] // dl[3] + (1 if dl[12] else 0)
+    return (din + 15) // 16 * 16
+
+
+def use_library_ops() -> bool:
+    """True while torch.compile traces or a Python dispatch mode (fake tensors,
+    FlopCounterMode, ...) is active."""
+    from torch.utils._python_dispatch import _get_current_dispatch_mode
+    return torch.compiler.is_compiling() or _get_current_dispatch_mode() is not None
+
+
+_EMPTY = lambda like: torch.empty((0,), dtype=torch.float32, device=like.device)
+
+
+@torch.library.custom_op("cnna::core", mutates_args=())
+def core_op(x: torch.Tensor, Wq: torch.Tensor, Wk: torch.Tensor, Wv: torch.Tensor, w0: torch.Tensor,
+            w1: Optional[torch.Tensor], cand: Optional[torch.Tensor], wmul: Optional[torch.Tensor],
+            desc: List[int], scale: float, reference_errors: bool
+            ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                       torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """x -> (z, q, k, v, qn, kn, idx, vals, w): projections, selection,
+    aggregation, head merge (layers.py:261-317); qn / kn empty when unused."""
+    d = _desc_of(desc, scale)
+    q, k, v, qn, kn = project_qkv(d, x, cand, Wq, Wk, Wv)
+    idx, vals, w = select(d, k, q, kn, qn, cand)
+    z = aggregate(d, v, idx, w if wmul is None else w * wmul, w0, w1)
+    return (z, q, k, v, _EMPTY(x) if qn is None else qn, _EMPTY(x) if kn is None else kn, idx, vals, w)
+
+
+@core_op.register_fake
+def _core_fake(x, Wq, Wk, Wv, w0, w1, cand, wmul, desc, scale, reference_errors):
+    B, N, C, H, Nq, K = desc[:6]
+    BH, dkp = B * H, _dkp(desc)
+    f32 = dict(dtype=torch.float32, device=x.device)
+    norms = desc[8] != METRICS["matmul"]
+    return (x.new_empty((B, N, C)), x.new_empty((BH, Nq, dkp)), x.new_empty((BH, N, dkp)),
+            x.new_empty((BH, N, dkp)), torch.empty((BH * Nq if norms else 0,), **f32),
+            torch.empty((BH * N if norms else 0,), **f32),
+            torch.empty((BH, N, K), dtype=torch.int32, device=x.device), torch.empty((BH, N, K), **f32),
+            torch.empty((BH, N, K), **f32))
+
+
+@torch.library.custom_op("cnna::core_backward", mutates_args=())
+def core_backward_op(x: torch.Tensor, Wq: torch.Tensor, Wk: torch.Tensor, Wv: torch.Tensor,
+                     w0: torch.Tensor, w1: Optional[torch.Tensor], cand: Optional[torch.Tensor],
+                     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qn: torch.Tensor, kn: torch.Tensor,
+                     idx: torch.Tensor, vals: torch.Tensor, w: torch.Tensor, wmul: Optional[torch.Tensor],
+                     dz: torch.Tensor, desc: List[int], scale: float
+                     ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                                torch.Tensor]:
+    """Gradients (dx, dWq, dWk, dWv, dw0, dw1) of ``cnna::core``; dw1 empty without w1."""
+    d = _desc_of(desc, scale)
+    nq = None if qn.numel() == 0 else qn
+    nk = None if kn.numel() == 0 else kn
+    dx, dWq, dWk, dWv, dw0, dw1 = core_backward(d, x, cand, Wq, Wk, Wv, w0, w1,
+                                                (q, k, v, nq, nk, idx, vals, w, wmul), dz)
+    return dx, dWq, dWk, dWv, dw0.to(w0.dtype), (x.new_empty((0,)) if dw1 is None else dw1.to(w1.dtype))
+
+
+@core_backward_op.register_fake
+def _core_backward_fake(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul, dz, desc, scale):
+    return (x.new_empty(x.shape), x.new_empty(Wq.shape), x.new_empty(Wk.shape), x.new_empty(Wv.shape),
+            w0.new_empty(w0.shape), (x.new_empty((0,)) if w1 is None else w1.new_empty(w1.shape)))
+
+
+def _core_setup(ctx, inputs, output):
+    x, Wq, Wk, Wv, w0, w1, cand, wmul, desc, scale, reference_errors = inputs
+    z, q, k, v, qn, kn, idx, vals, w = output
+    ctx.desc, ctx.scale, ctx.reference_errors = desc, scale, reference_errors
+    ctx.has_w1 = w1 is not None
+    ctx.save_for_backward(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul)
+
+
+def _core_bwd(ctx, dz, *unused):
+    dl = ctx.desc
+    if ctx.reference_errors and dl[11] and dl[8] == METRICS["euclidean"]:
+        raise RuntimeError(
+            "one of the variables needed for gradient computation has been modified by an "
+            "inplace operation: the sampled euclidean similarity is masked in place after "
+            "sqrt (layers.py:291-292, 304-305)")
+    x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul = ctx.saved_tensors
+    dx, dWq, dWk, dWv, dw0, dw1 = core_backward_op(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx,
+                                                   vals, w, wmul, dz.contiguous(), dl, ctx.scale)
+    return dx, dWq, dWk, dWv, dw0, (dw1 if ctx.has_w1 else None), None, None, None, None, None
+
+
+torch.library.register_autograd("cnna::core", _core_bwd, setup_context=_core_setup)
+
+
+@torch.library.custom_op("cnna::output_proj", mutates_args=())
+def output_proj_op(z: torch.Tensor, Wo: torch.Tensor, desc: List[int], scale: float) -> torch.Tensor:
+    """out = z @ Wo^T (layers.py:320)."""
+    return output_proj(_desc_of(desc, scale), z, Wo)
+
+
+@output_proj_op.register_fake
+def _output_proj_fake(z, Wo, desc, scale):
+    return z.new_empty((desc[0], desc[1], desc[2]))
+
+
+@torch.library.custom_op("cnna::output_proj_backward", mutates_args=())
+def output_proj_backward_op(z: torch.Tensor, Wo: torch.Tensor, dout: torch.Tensor, desc: List[int],
+                            scale: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    return output_proj_backward(_desc_of(desc, scale), z, Wo, dout)
+
+
+@output_proj_backward_op.register_fake
+def _output_proj_backward_fake(z, Wo, dout, desc, scale):
+    return z.new_empty(z.shape), Wo.new_empty(Wo.shape)
+
+
+def _oproj_setup(ctx, inputs, output):
+    z, Wo, desc, scale = inputs
+    ctx.desc, ctx.scale = desc, scale
+    ctx.save_for_backward(z, Wo)
+
+
+def _oproj_bwd(ctx, dout):
+    z, Wo = ctx.saved_tensors
+    dz, dWo = output_proj_backward_op(z, Wo, dout.contiguous(), ctx.desc, ctx.scale)
+    return dz, dWo, None, None
+
+
+torch.library.register_autograd("cnna::output_proj", _oproj_bwd, setup_context=_oproj_setup)
+
+
+# ---- FLOP formulas (2 per multiply-accumulate, the work the reference's ops do)
+def core_flops(desc) -> int:
+    """Projections, similarity and conv of one forward (layers.py:264-313)."""
+    B, N, C, H, Nq, K = desc[:6]
+    conv = desc[9]
+    dk = C // H
+    din = dk + (1 if desc[12] else 0)
+    proj = 2 * B * C * C * (2 * N + Nq)
+    sim = 2 * B * N * Nq * H * din
+    if conv == CONVS["depthwise"]:
+        cv = 2 * B * N * H * dk * K
+    elif conv == CONVS["standard"]:
+        cv = 2 * B * N * H * dk * din * K
+    else:
+        cv = 2 * B * N * H * (din * K + dk * din)
+    return proj + sim + cv
+
+
+def _register_flops():
+    from torch.utils.flop_counter import register_flop_formula
+
+    @register_flop_formula(torch.ops.cnna.core)
+    def _f_core(x, Wq, Wk, Wv, w0, w1, cand, wmul, desc, scale, reference_errors, *a, out_shape=None, **kw):
+        return core_flops(desc)
+
+    @register_flop_formula(torch.ops.cnna.core_backward)
+    def _f_core_bwd(*args, out_shape=None, **kw):
+        return 2 * core_flops(args[17])
+
+    @register_flop_formula(torch.ops.cnna.output_proj)
+    def _f_oproj(z, Wo, desc, scale, *a, out_shape=None, **kw):
+        return 2 * desc[0] * desc[1] * desc[2] * desc[2]
+
+    @register_flop_formula(torch.ops.cnna.output_proj_backward)
+    def _f_oproj_bwd(z, Wo, dout, desc, scale, *a, out_shape=None, **kw):
+        return 4 * desc[0] * desc[1] * desc[2] * desc[2]
+
+
+_register_flops()

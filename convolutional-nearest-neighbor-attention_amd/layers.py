@@ -106,11 +106,17 @@ class MultiHeadConvNNAttention(nn.Module):
 
     def forward(self, x):
         z, d = self.core(x)
-        return ops.OutputProj.apply(z, self.W_o.weight, d)
+        Wo = _amp_cast(self.W_o.weight, z.dtype)
+        if isinstance(d, list):
+            return torch.ops.cnna.output_proj(z, Wo, d, 0.0)
+        return ops.OutputProj.apply(z, Wo, d)
 
     def core(self, x):
         """Everything before W_o (layers.py:261-317): returns (z, desc), z the
-        merged conv output after dropout."""
+        merged conv output after dropout.  Under torch.autocast the layer
+        computes in bfloat16 (its kernels' reduced precision); while compiling
+        or under a dispatch mode it runs as the ``cnna::`` library ops and the
+        descriptor is a list of ints."""
         if x.dim() != 3:
             raise RuntimeError(f"expected x of shape (B, N, C), got {tuple(x.shape)}")
         if not x.is_cuda:
@@ -119,23 +125,48 @@ class MultiHeadConvNNAttention(nn.Module):
         self.batch_size = B                                                          # layers.py:239
         cand = self._candidates(x)
         Nq = N if cand is None else int(cand.numel())
-        if self.W_q.weight.dtype != x.dtype:
+        x, Wq, Wk, Wv = _amp_inputs(x, self.W_q.weight, self.W_k.weight, self.W_v.weight)
+        if Wq.dtype != x.dtype:
             raise RuntimeError(f"mat1 and mat2 must have the same dtype, but got {x.dtype} and "
-                               f"{self.W_q.weight.dtype}")
+                               f"{Wq.dtype}")
+        w0, w1 = self._conv_weights()
+        if ops.use_library_ops():
+            d = ops.desc_values(B, N, C, self.num_heads, Nq, self.K, self.seq_length, x.dtype,
+                                self.magnitude_type, self.convolution_type, self.softmax_topk_val,
+                                cand is not None, self.coordinate_encoding)
+            z = torch.ops.cnna.core(x, Wq, Wk, Wv, _amp_cast(w0, x.dtype), _amp_cast(w1, x.dtype), cand,
+                                    None, d, 0.0, True)[0]
+            return self.dropout(z), d
         d = ops.make_desc(B, N, C, self.num_heads, Nq, self.K, self.seq_length, x.dtype,
                           self.magnitude_type, self.convolution_type, self.softmax_topk_val,
                           cand is not None, self.coordinate_encoding)
-        w0, w1 = self._conv_weights()
-        z = ops.ConvNNCore.apply(x, self.W_q.weight, self.W_k.weight, self.W_v.weight, w0, w1, cand, d,
-                                 True)
+        z = ops.ConvNNCore.apply(x, Wq, Wk, Wv, w0, w1, cand, d, True)
         # dropout on the conv output (layers.py:316); elementwise, so applying it
         # after the head merge is the same operation on permuted elements
         return self.dropout(z), d
 
 
+AMP_DTYPE = torch.bfloat16
+
+
+def _amp_cast(t, dtype):
+    return t if t is None or t.dtype == dtype else t.to(dtype)
+
+
+def _amp_inputs(x, *weights):
+    """Autocast policy of the native layers: inside ``torch.autocast('cuda')``
+    (the reference's ``--use_amp`` loop, train_eval.py:137-146) x and the
+    weights are cast to bfloat16, the reduced type the kernels compute in,
+    whatever autocast's own dtype; gradients flow back through the casts."""
+    if torch.is_autocast_enabled("cuda"):
+        return (_amp_cast(x, AMP_DTYPE),) + tuple(_amp_cast(w, AMP_DTYPE) for w in weights)
+    return (x,) + weights
+
+
 def _inference(module: nn.Module, x: torch.Tensor) -> bool:
-    """Nothing to differentiate: the native inference kernels may run."""
-    if not x.is_cuda:
+    """Nothing to differentiate, no autocast, not tracing: the fused native
+    inference kernels may run."""
+    if not x.is_cuda or torch.is_autocast_enabled("cuda") or ops.use_library_ops():
         return False
     if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in module.parameters())):
         return False
@@ -377,15 +408,21 @@ class MultiHeadKvtAttention(nn.Module):
             raise RuntimeError("selected index k out of range")                # torch.topk
         if self.topk > 32:
             raise NotImplementedError("cnna: MultiHeadKvtAttention supports topk <= 32")
-        if self.qkv.weight.dtype != x.dtype:
+        x, W, P = _amp_inputs(x, self.qkv.weight, self.proj.weight)
+        if W.dtype != x.dtype:
             raise RuntimeError(f"mat1 and mat2 must have the same dtype, but got {x.dtype} and "
-                               f"{self.qkv.weight.dtype}")
-        d = ops.make_desc(B, N, C, H, N, self.topk, N, x.dtype, "matmul", "depthwise", True, False, False,
-                          merge=ops.MERGE_CONCAT, scale=self.scale)
-        W = self.qkv.weight
+                               f"{W.dtype}")
         ones = torch.ones((C // H, 1, self.topk), dtype=x.dtype, device=x.device)
         wmul = None
         if self.training and self.attn_drop.p > 0:
             wmul = self.attn_drop(torch.ones((B * H, N, self.topk), dtype=torch.float32, device=x.device))
+        if ops.use_library_ops():
+            d = ops.desc_values(B, N, C, H, N, self.topk, N, x.dtype, "matmul", "depthwise", True, False,
+                                False, merge=ops.MERGE_CONCAT)
+            z = torch.ops.cnna.core(x, W[C:2 * C], W[:C], W[2 * C:], ones, None, None, wmul, d,
+                                    float(self.scale), False)[0]
+            return self.proj_drop(torch.ops.cnna.output_proj(z, P, d, float(self.scale)))
+        d = ops.make_desc(B, N, C, H, N, self.topk, N, x.dtype, "matmul", "depthwise", True, False, False,
+                          merge=ops.MERGE_CONCAT, scale=self.scale)
         z = ops.ConvNNCore.apply(x, W[C:2 * C], W[:C], W[2 * C:], ones, None, None, d, False, wmul)
-        return self.proj_drop(ops.OutputProj.apply(z, self.proj.weight, d))
+        return self.proj_drop(ops.OutputProj.apply(z, P, d))

@@ -11,8 +11,9 @@ operator on a channel slice beside a Conv1d or softmax-attention branch),
 ``Attention``; the reference's Local / Neighborhood / Sparse attention
 families are outside this operator's scope and raise ValueError.
 
-In inference (eval mode, no gradients) each block runs with its prologue and
-epilogues fused: LayerNorm kernels, W_o + residual (ConvNN attention) or the
+In inference (eval mode, no gradients, no autocast, not being traced) each
+block runs with its prologue and epilogues fused: LayerNorm kernels, W_o +
+residual (ConvNN attention) or the
 residual add inside the second LayerNorm (other layers), fc1 + bias + GELU and
 fc2 + bias + residual in the GEMM epilogues (cnna_layernorm, cnna_linear).
 Training and autograd use the composable modules.
@@ -52,7 +53,8 @@ class PatchEmbedding(nn.Module):
         self.flatten = nn.Flatten(start_dim=2)
 
     def forward(self, x):
-        if x.is_cuda and not self.training and not torch.is_grad_enabled() and self.norm.weight.dtype == x.dtype:
+        if (x.is_cuda and not self.training and not torch.is_grad_enabled() and self.norm.weight.dtype == x.dtype
+                and not torch.is_autocast_enabled("cuda") and not ops.use_library_ops()):
             # inference: the stride = kernel convolution is a GEMM over the patches
             # (one permuting copy, the MFMA GEMM with its bias, the LayerNorm kernel)
             conv = self.linear_projection
@@ -126,7 +128,7 @@ class TransformerEncoder(nn.Module):
 
     def _fusable(self, x):
         """Inference on the GPU: dropout inactive and nothing to differentiate."""
-        if self.training or not x.is_cuda:
+        if self.training or not x.is_cuda or torch.is_autocast_enabled("cuda") or ops.use_library_ops():
             return False
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
             return False
