@@ -50,6 +50,17 @@ template <> struct Row<uint16_t, 4> {
     o[3] = __uint_as_float(u.y & 0xffff0000u);
   }
 };
+template <> struct Row<uint16_t, 8> {
+  static CNNA_DEV void load(const uint16_t* p, float (&o)[8]) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+};
 template <> struct Row<float, 1> {
   static CNNA_DEV void load(const float* p, float (&o)[1]) { o[0] = *p; }
 };
@@ -110,6 +121,19 @@ __global__ __launch_bounds__(256) void unmerge_kernel(const T* dz, T* dy, int BH
 }
 
 // ------------------------------------------------------------------ tok_bwd
+template <int CTRL>
+CNNA_DEV float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// sum over the 16 lanes of a DPP row (every lane gets the row's sum)
+CNNA_DEV float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+  v += dpp_f<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+  v += dpp_f<0x141>(v);   // row_half_mirror
+  v += dpp_f<0x140>(v);   // row_mirror
+  return v;
+}
+
 template <typename T, int CPL, int KMAX, bool DW>
 __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
   constexpr int CW = 64 * CPL;
@@ -133,6 +157,7 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
 
   const bool euc = a.metric == CNNA_EUCLIDEAN, cos_ = a.metric == CNNA_COSINE;
   const bool gvec = (a.din % CPL) == 0;
+  const bool svec = (a.din % (16 / (int)sizeof(T))) == 0;   // 16-byte rows of dP and v
   const int ntok = a.BH * a.N;
   const int nw = gridDim.x * 4;
   for (int tok = blockIdx.x * 4 + wv; tok < ntok; tok += nw) {
@@ -155,9 +180,43 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
 
     // dw[r] = sum_c dP[c, r] * v[c, idx[r]]
     float my_dw = 0.0f;
+    if (!DW && svec) {
+      // standard conv: four neighbours per pass, 16 lanes per neighbour row
+      // with 16-byte loads of dP and v, row sums by DPP inside the 16 lanes
+      constexpr int V16 = 16 / sizeof(T);
+      constexpr int NP = (64 * CPL + 16 * V16 - 1) / (16 * V16);
+      const int grp = lane >> 4, gl = lane & 15;
+#pragma unroll
+      for (int r0 = 0; r0 < KMAX; r0 += 4) {
+        if (r0 < K) {
+          const int rr = min(r0 + grp, K - 1);
+          const int t = __shfl(my_j, rr);
+          const T* vrow = V + (int64_t)t * a.dkp;
+          const T* prow = static_cast<const T*>(a.dP) + (ebase + rr) * a.din;
+          float acc = 0.0f;
+#pragma unroll
+          for (int ps = 0; ps < NP; ++ps) {
+            const int c = (ps * 16 + gl) * V16;
+            if (c < a.din) {
+              float vv[V16], pp[V16];
+              Row<T, V16>::load(vrow + c, vv);
+              Row<T, V16>::load(prow + c, pp);
+#pragma unroll
+              for (int u = 0; u < V16; ++u) acc += pp[u] * vv[u];
+            }
+          }
+          acc = row16_sum(acc);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float sq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 16 * q));
+            if (lane == r0 + q) my_dw = sq;
+          }
+        }
+      }
+    }
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) {
-      if (r < K) {
+      if (r < K && (DW || !svec)) {
         const int t = __builtin_amdgcn_readlane(my_j, r);
         float vv[CPL];
         load_row<T, CPL>(V + (int64_t)t * a.dkp, c0, a.dkp, true, vv);
