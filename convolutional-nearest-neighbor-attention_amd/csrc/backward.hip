@@ -120,6 +120,30 @@ __global__ __launch_bounds__(256) void unmerge_kernel(const T* dz, T* dy, int BH
   dy[e] = dz[src];
 }
 
+// Mixing case (H > 1, reference merge) as a tiled transpose: for one (b, h),
+// y_bh viewed as (dk, N) [a][t] is the transpose of the (N, dk) slice
+// Z[b, :, h*dk : (h+1)*dk].  64 x 64 tiles through LDS: reads run along the
+// channels, writes along the tokens, both coalesced.
+template <typename T>
+__global__ __launch_bounds__(256) void unmerge_tile_kernel(const T* dz, T* dy, int N, int dk, int H,
+                                                           int C) {
+  __shared__ T tile[64][65];
+  const int bh = blockIdx.z, b = bh / H, h = bh - b * H;
+  const int t0 = blockIdx.x * 64, a0 = blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const T* src = dz + (int64_t)b * N * C + h * dk;
+  for (int r = ty; r < 64; r += 4) {
+    const int t = t0 + r, a = a0 + tx;
+    if (t < N && a < dk) tile[r][tx] = src[(int64_t)t * C + a];
+  }
+  __syncthreads();
+  T* dst = dy + (int64_t)bh * N * dk;
+  for (int r = ty; r < 64; r += 4) {
+    const int a = a0 + r, t = t0 + tx;
+    if (t < N && a < dk) dst[(int64_t)a * N + t] = tile[tx][r];
+  }
+}
+
 // ------------------------------------------------------------------ tok_bwd
 template <int CTRL>
 CNNA_DEV float dpp_f(float x) {
@@ -615,6 +639,18 @@ int launch_unmerge(int dtype, const void* dz, void* dy, int BH, int N, int dk, i
                    int concat, hipStream_t s) {
   const int64_t n = (int64_t)BH * N * dk;
   if (n <= 0) return 0;
+  if (H > 1 && !concat && BH <= 65535) {
+    const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((dk + 63) / 64), (unsigned)BH);
+    if (dtype == CNNA_BF16)
+      hipLaunchKernelGGL(unmerge_tile_kernel<uint16_t>, grid, dim3(256), 0, s,
+                         static_cast<const uint16_t*>(dz), static_cast<uint16_t*>(dy), N, dk, H, C);
+    else if (dtype == CNNA_F32)
+      hipLaunchKernelGGL(unmerge_tile_kernel<float>, grid, dim3(256), 0, s,
+                         static_cast<const float*>(dz), static_cast<float*>(dy), N, dk, H, C);
+    else
+      return CNNA_ERR_DTYPE;
+    return (int)hipGetLastError();
+  }
   if (dtype == CNNA_BF16)
     hipLaunchKernelGGL(unmerge_kernel<uint16_t>, grid_for(n), dim3(256), 0, s,
                        static_cast<const uint16_t*>(dz), static_cast<uint16_t*>(dy), BH, N, dk, H, C, concat);
