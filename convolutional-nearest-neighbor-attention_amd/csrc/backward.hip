@@ -588,12 +588,158 @@ __global__ __launch_bounds__(256) void pull_kernel(PullArgs a) {
   }
 }
 
+// Same sums with four keys per wave: a 16-lane group owns one key and walks
+// its entries in list order with 16-byte row loads (NP passes of 16 * V16
+// channels); the cosine row dot product is a DPP row sum.  Rows of dP / g and
+// k must be whole 16-byte vectors (din % V16 == 0).
+template <typename T, int CPL>
+__global__ __launch_bounds__(256) void pull16_kernel(PullArgs a) {
+  constexpr int V16 = 16 / sizeof(T);
+  constexpr int NP = (64 * CPL + 16 * V16 - 1) / (16 * V16);
+  constexpr int CW = 64 * CPL;
+  extern __shared__ float sW[];                   // depthwise: W0 as [r][c]
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int grp = lane >> 4, gl = lane & 15;
+  const bool dwv = a.do_v && !a.std_conv;
+  if (dwv) {
+    const T* W0 = static_cast<const T*>(a.w0);
+    for (int e = tid; e < a.K * CW; e += 256) {
+      const int r = e / CW, c = e - r * CW;
+      sW[e] = c < a.din ? ldf(W0 + c * a.K + r) : 0.0f;
+    }
+    __syncthreads();
+  }
+  const int64_t nk = (int64_t)a.BH * a.nkeys;
+  const int64_t gk = ((int64_t)blockIdx.x * 4 + wv) * 4 + grp;
+  const bool kvalid = gk < nk;
+  const int64_t gkc = kvalid ? gk : nk - 1;      // idle groups walk a real key, store nothing
+  const int bh = (int)(gkc / a.nkeys), key = (int)(gkc - (int64_t)bh * a.nkeys);
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int64_t NK = (int64_t)a.N * a.K;
+  const int32_t* off = a.off + (int64_t)bh * (a.nkeys + 1);
+  const int beg = off[key], end = off[key + 1];
+  const int32_t* list = a.list + bh * NK;
+  const T* G = static_cast<const T*>(a.g);
+  const T* DP = static_cast<const T*>(a.dP);
+  const T* Kt = static_cast<const T*>(a.k) + (int64_t)bh * a.N * a.dkp;
+
+  float dv[NP][V16], dq[NP][V16], cs = 0.0f;
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int u = 0; u < V16; ++u) dv[p][u] = dq[p][u] = 0.0f;
+  for (int x = beg; x < end; ++x) {
+    const int e = list[x];
+    const int i = e / a.K, r = e - i * a.K;
+    if (a.do_v) {
+      const float we = a.w[bh * NK + e] * (a.wmul != nullptr ? a.wmul[bh * NK + e] : 1.0f);
+      const T* row = a.std_conv ? DP + (bh * NK + e) * a.din : G + ((int64_t)bh * a.N + i) * a.din;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int c = (p * 16 + gl) * V16;
+        if (c < a.din) {
+          float gg[V16];
+          Row<T, V16>::load(row + c, gg);
+          if (a.std_conv) {
+#pragma unroll
+            for (int u = 0; u < V16; ++u) dv[p][u] += we * gg[u];
+          } else {
+#pragma unroll
+            for (int u = 0; u < V16; ++u) dv[p][u] += we * (sW[r * CW + c + u] * gg[u]);
+          }
+        }
+      }
+    }
+    if (a.do_q) {
+      const float ce = a.coef[bh * NK + e];
+      if (ce != 0.0f) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const int c = (p * 16 + gl) * V16;
+          if (c < a.dkp) {
+            float kk[V16];
+            Row<T, V16>::load(Kt + (int64_t)i * a.dkp + c, kk);
+#pragma unroll
+            for (int u = 0; u < V16; ++u) dq[p][u] += ce * kk[u];
+          }
+        }
+        cs += ce;
+      }
+    }
+  }
+  if (a.do_v && kvalid) {
+    T* dst = static_cast<T*>(a.dst_v) + ((int64_t)b * a.N + key) * a.ld_v + a.off_v + h * a.dk;
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int u = 0; u < V16; ++u) {
+        const int c = (p * 16 + gl) * V16 + u;
+        if (c < a.dk) stf(dst + c, dv[p][u]);
+      }
+  }
+  if (a.do_q) {
+    if (a.metric != CNNA_MATMUL) {
+      const T* qrow = static_cast<const T*>(a.q) + ((int64_t)bh * a.nkeys + key) * a.dkp;
+      float qv[NP][V16];
+      float d = 0.0f;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int c = (p * 16 + gl) * V16;
+        if (c < a.dkp) {
+          Row<T, V16>::load(qrow + c, qv[p]);
+        } else {
+#pragma unroll
+          for (int u = 0; u < V16; ++u) qv[p][u] = 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < V16; ++u) d += qv[p][u] * dq[p][u];
+      }
+      if (a.metric == CNNA_COSINE) {
+        d = row16_sum(d);
+        const float nrm = sqrtf(a.qn[(int64_t)bh * a.nkeys + key]);
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+          for (int u = 0; u < V16; ++u)
+            dq[p][u] = nrm > 1e-12f ? (dq[p][u] - qv[p][u] * d) / nrm : dq[p][u] / 1e-12f;
+      } else {
+        // q * sum(coef) - sum(coef * k)
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+          for (int u = 0; u < V16; ++u) dq[p][u] = qv[p][u] * cs - dq[p][u];
+      }
+    }
+    if (kvalid) {
+      T* dst = static_cast<T*>(a.dst_q) + ((int64_t)b * a.nkeys + key) * a.ld_q + a.off_q + h * a.dk;
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int u = 0; u < V16; ++u) {
+          const int c = (p * 16 + gl) * V16 + u;
+          if (c < a.dk) stf(dst + c, dq[p][u]);
+        }
+    }
+  }
+}
+
 template <typename T>
 int launch_pull_t(const PullArgs& a, hipStream_t s) {
   const int64_t waves = (int64_t)a.BH * a.nkeys;
   if (waves <= 0) return 0;
   dim3 grid((unsigned)((waves + 3) / 4));
   auto lds = [&](int cpl) { return (size_t)((a.do_v && !a.std_conv) ? a.K * 64 * cpl * 4 : 0); };
+  constexpr int V16 = 16 / sizeof(T);
+  if (a.din % V16 == 0 && a.dkp <= 256) {
+    const dim3 grid16((unsigned)((waves + 15) / 16));
+    if (a.dkp <= 64)
+      hipLaunchKernelGGL((pull16_kernel<T, 1>), grid16, dim3(256), lds(1), s, a);
+    else if (a.dkp <= 128)
+      hipLaunchKernelGGL((pull16_kernel<T, 2>), grid16, dim3(256), lds(2), s, a);
+    else
+      hipLaunchKernelGGL((pull16_kernel<T, 4>), grid16, dim3(256), lds(4), s, a);
+    return (int)hipGetLastError();
+  }
   if (a.dkp <= 64)
     hipLaunchKernelGGL((pull_kernel<T, 1>), grid, dim3(256), lds(1), s, a);
   else if (a.dkp <= 128)
