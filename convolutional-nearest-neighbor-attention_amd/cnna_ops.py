@@ -83,7 +83,11 @@ def _load():
     return lib
 
 
+ABI_VERSION = 2        # CNNA_ABI_VERSION of the include/cnna.h this binding mirrors
 LIB = _load()
+if LIB.cnna_abi_version() != ABI_VERSION:
+    raise ImportError(f"libcnna.so ABI {LIB.cnna_abi_version()} != {ABI_VERSION}: rebuild it with "
+                      "`python convolutional-nearest-neighbor-attention_amd/build.py`")
 EXPORTED = ("cnna_abi_version", "cnna_error_string", "cnna_check_desc", "cnna_head_stride",
             "cnna_project_qkv", "cnna_select", "cnna_aggregate_workspace", "cnna_aggregate",
             "cnna_output_proj", "cnna_forward_workspace", "cnna_forward",
