@@ -13,6 +13,7 @@ import os
 from typing import List, Optional, Tuple
 
 import torch
+from torch.utils._python_dispatch import _get_current_dispatch_mode
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libcnna.so")
@@ -424,7 +425,6 @@ def _dkp(dl) -> int:
 def use_library_ops() -> bool:
     """True while torch.compile traces or a Python dispatch mode (fake tensors,
     FlopCounterMode, ...) is active."""
-    from torch.utils._python_dispatch import _get_current_dispatch_mode
     return torch.compiler.is_compiling() or _get_current_dispatch_mode() is not None
 
 
