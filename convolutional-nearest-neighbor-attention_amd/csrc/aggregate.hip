@@ -63,8 +63,8 @@ template <typename T> struct Vec<T, 1> {
   static CNNA_DEV void store(T* p, const float (&o)[1]) { stf(p, o[0]); }
 };
 
-// KM > 0: K <= KM, and all K neighbour rows of a token are loaded before
-// any is used (one memory latency per token instead of K)
+// KM > 0: K <= KM, and all K neighbour rows of two tokens are loaded before
+// any is used (one memory latency per two tokens instead of K per token)
 template <typename T, int VW, bool COPY, int KM>
 __global__ __launch_bounds__(256) void agg_kernel(AggArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -107,41 +107,8 @@ __global__ __launch_bounds__(256) void agg_kernel(AggArgs a) {
   const T* V = static_cast<const T*>(a.v) + (int64_t)bh * a.N * a.dkp;
   const int b = bh / a.H, h = bh - b * a.H;
 
-  for (int tt = tid / LPT; tt < ntok; tt += 256 / LPT) {
-    if (c0 >= dout) continue;
-    const int i = i0 + tt;
-    float acc[VW];
-    if (COPY) {
-      Vec<T, VW>::load(static_cast<const T*>(a.v) + ((int64_t)bh * a.N + i) * dout + c0, acc);
-    } else if constexpr (KM > 0) {
-#pragma unroll
-      for (int u = 0; u < VW; ++u) acc[u] = 0.0f;
-      typename Vec<T, VW>::Raw raw[KM > 0 ? KM : 1];
-#pragma unroll
-      for (int r = 0; r < KM; ++r)
-        if (r < a.K) raw[r] = Vec<T, VW>::raw(V + (int64_t)sj[tt * a.K + r] * a.dkp + c0);
-#pragma unroll
-      for (int r = 0; r < KM; ++r) {
-        if (r < a.K) {
-          const float wr = sw[tt * a.K + r];
-          float vv[VW];
-          Vec<T, VW>::unpack(raw[r], vv);
-#pragma unroll
-          for (int u = 0; u < VW; ++u) acc[u] += sW[r * dout + c0 + u] * (wr * vv[u]);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < VW; ++u) acc[u] = 0.0f;
-      for (int r = 0; r < a.K; ++r) {
-        const int j = sj[tt * a.K + r];
-        const float wr = sw[tt * a.K + r];
-        float vv[VW];
-        Vec<T, VW>::load(V + (int64_t)j * a.dkp + c0, vv);
-#pragma unroll
-        for (int u = 0; u < VW; ++u) acc[u] += sW[r * dout + c0 + u] * (wr * vv[u]);
-      }
-    }
+  // one token's conv output (VW channels from c0) to Z / the staged range / y
+  auto emit = [&](int i, const float (&acc)[VW]) __attribute__((always_inline)) {
     if (stage_z) {
       const int64_t f0 = (int64_t)i * dout + c0;
       int aa = (int)(f0 / a.N);
@@ -161,6 +128,68 @@ __global__ __launch_bounds__(256) void agg_kernel(AggArgs a) {
       Vec<T, VW>::store(static_cast<T*>(a.out) + ((int64_t)b * a.N + i) * a.C + h * dout + c0, acc);
     } else {
       Vec<T, VW>::store(static_cast<T*>(a.out) + ((int64_t)bh * a.N + i) * dout + c0, acc);
+    }
+  };
+
+  if constexpr (!COPY && KM > 0) {
+    // two tokens per pass: the K neighbour rows of both are in flight at once
+    typedef typename Vec<T, VW>::Raw Raw;
+    const int step = 256 / LPT;
+    auto conv = [&](int tt, const Raw (&raw)[KM], float (&acc)[VW]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < VW; ++u) acc[u] = 0.0f;
+#pragma unroll
+      for (int r = 0; r < KM; ++r) {
+        if (r < a.K) {
+          const float wr = sw[tt * a.K + r];
+          float vv[VW];
+          Vec<T, VW>::unpack(raw[r], vv);
+#pragma unroll
+          for (int u = 0; u < VW; ++u) acc[u] += sW[r * dout + c0 + u] * (wr * vv[u]);
+        }
+      }
+    };
+    for (int tt = tid / LPT; tt < ntok; tt += 2 * step) {
+      if (c0 >= dout) continue;
+      const int tt2 = tt + step;
+      const bool two = tt2 < ntok;
+      Raw raw[KM], raw2[KM];
+#pragma unroll
+      for (int r = 0; r < KM; ++r)
+        if (r < a.K) raw[r] = Vec<T, VW>::raw(V + (int64_t)sj[tt * a.K + r] * a.dkp + c0);
+      if (two) {
+#pragma unroll
+        for (int r = 0; r < KM; ++r)
+          if (r < a.K) raw2[r] = Vec<T, VW>::raw(V + (int64_t)sj[tt2 * a.K + r] * a.dkp + c0);
+      }
+      float acc[VW];
+      conv(tt, raw, acc);
+      emit(i0 + tt, acc);
+      if (two) {
+        conv(tt2, raw2, acc);
+        emit(i0 + tt2, acc);
+      }
+    }
+  } else {
+    for (int tt = tid / LPT; tt < ntok; tt += 256 / LPT) {
+      if (c0 >= dout) continue;
+      const int i = i0 + tt;
+      float acc[VW];
+      if (COPY) {
+        Vec<T, VW>::load(static_cast<const T*>(a.v) + ((int64_t)bh * a.N + i) * dout + c0, acc);
+      } else {
+#pragma unroll
+        for (int u = 0; u < VW; ++u) acc[u] = 0.0f;
+        for (int r = 0; r < a.K; ++r) {
+          const int j = sj[tt * a.K + r];
+          const float wr = sw[tt * a.K + r];
+          float vv[VW];
+          Vec<T, VW>::load(V + (int64_t)j * a.dkp + c0, vv);
+#pragma unroll
+          for (int u = 0; u < VW; ++u) acc[u] += sW[r * dout + c0 + u] * (wr * vv[u]);
+        }
+      }
+      emit(i, acc);
     }
   }
   if (!stage_z) return;
