@@ -190,12 +190,22 @@ int cnna_core_backward(const cnna_desc* d, const void* x, int64_t ldx, const int
   } else {
     // standard: dP = dy @ W0p ; dW0p = dy^T P with P[tok][r*din + c] = w * v[idx] gathered
     // inside the GEMM, permuted back to (dk, din, K)
-    if ((st = launch_permute_w0(dt, conv_w0, p.w0p, dk, din, K, s))) return st;
-    GradGemmArgs g = gg(ntok, K * din, dk, p.dy, dk, GG_ROWS, p.w0p, (int64_t)K * din, GG_TRANS);
-    g.o = p.dP;
-    g.ldo = (int64_t)K * din;
-    if ((st = launch_gemm_grad(dt, g, s))) return st;
-    g = gg(dk, K * din, ntok, p.dy, dk, GG_TRANS, sv->v, 0, GG_GATHER_T);
+    // dP as a row GEMM against W0p^T (the forward kernel: LDS-staged 16-byte stores
+    // of the 805 MB-class output)
+    if ((st = launch_permute_w0t(dt, conv_w0, p.w0p, dk, din, K, s))) return st;
+    {
+      const int es = elem_size(dt);
+      GemmArgs f;
+      memset(&f, 0, sizeof(f));
+      f.M = ntok; f.Nc = K * din; f.Kd = dk;
+      f.a = p.dy; f.lda = dk;
+      f.avec = ((dk * es) % 16 == 0) && aligned16(p.dy);
+      f.w[0] = p.w0p; f.ncol_each = K * din;
+      f.bvec = ((dk * es) % 16 == 0) && aligned16(p.w0p);
+      f.o[0] = p.dP; f.ldo = (int64_t)K * din;
+      if ((st = launch_gemm(dt, GEMM_A_ROWS, GEMM_O_PLAIN, f, s))) return st;
+    }
+    GradGemmArgs g = gg(dk, K * din, ntok, p.dy, dk, GG_TRANS, sv->v, 0, GG_GATHER_T);
     g.g_idx = sv->idx; g.g_w = sv->w; g.g_K = K; g.g_N = N; g.g_din = din; g.g_dkp = dkp;
     if ((st = weight_grad(dt, g, p.part, gr->dconv_w0, nullptr, nullptr, dk, (int64_t)din * K, din,
                           K, s)))

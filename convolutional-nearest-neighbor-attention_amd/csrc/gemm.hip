@@ -463,7 +463,34 @@ __global__ void permute_w0_kernel(const T* w0, T* w0p, int dout, int din, int K)
   w0p[(int64_t)o * din * K + (int64_t)r * din + c] = w0[e];
 }
 
+// W0 (dout, din, K) -> W0t (K*din, dout) with W0t[r*din + c][o] = W0[o][c][r]:
+// the transpose of W0p, the weight operand of dP = dy @ W0p as a row GEMM
+template <typename T>
+__global__ void permute_w0t_kernel(const T* w0, T* w0t, int dout, int din, int K) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = (int64_t)dout * din * K;
+  if (e >= total) return;
+  const int o = (int)(e / ((int64_t)din * K));
+  const int rem = (int)(e - (int64_t)o * din * K);
+  const int c = rem / K, r = rem - c * K;
+  w0t[((int64_t)r * din + c) * dout + o] = w0[e];
+}
+
 }  // namespace
+
+int launch_permute_w0t(int dtype, const void* w0, void* w0t, int dout, int din, int K, hipStream_t s) {
+  const int64_t total = (int64_t)dout * din * K;
+  dim3 grid((unsigned)((total + 255) / 256));
+  if (dtype == CNNA_BF16)
+    hipLaunchKernelGGL(permute_w0t_kernel<uint16_t>, grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(w0), static_cast<uint16_t*>(w0t), dout, din, K);
+  else if (dtype == CNNA_F32)
+    hipLaunchKernelGGL(permute_w0t_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(w0),
+                       static_cast<float*>(w0t), dout, din, K);
+  else
+    return CNNA_ERR_DTYPE;
+  return (int)hipGetLastError();
+}
 
 int launch_gemm(int dtype, int amode, int omode, const GemmArgs& g, hipStream_t s) {
   if (g.M <= 0 || g.Nc <= 0 || g.Kd <= 0) return 0;
