@@ -454,6 +454,65 @@ __global__ __launch_bounds__(256) void csr_fill_kernel(CsrArgs c) {
   c.tmp[(int64_t)bh * NK + c.off[(int64_t)bh * (c.nkeys + 1) + key] + pos] = e;
 }
 
+// One block per (b, h) with the key counters in LDS: count, exclusive scan,
+// then the bucket fill with LDS cursors (bucket order arbitrary; the rank sort
+// below restores entry order).  Four entries per thread and step, their
+// loads issued before the LDS atomics.
+constexpr int CSR_LDS_MAX_KEYS = 16384;
+__global__ __launch_bounds__(1024) void csr_lds_kernel(CsrArgs c) {
+  extern __shared__ int sc[];                      // nkeys counters, then 1024 scan partials
+  int* part = sc + c.nkeys;
+  const int bh = blockIdx.x, tid = threadIdx.x;
+  const int64_t NK = (int64_t)c.N * c.K;
+  const int nk = (int)NK;
+  for (int k = tid; k < c.nkeys; k += 1024) sc[k] = 0;
+  __syncthreads();
+  auto walk = [&](auto visit) __attribute__((always_inline)) {
+    for (int e0 = 0; e0 < nk; e0 += 4 * 1024) {
+      int key[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = e0 + j * 1024 + tid;
+        key[j] = -1;
+        if (e < nk) {
+          const int i = e / c.K, r = e - i * c.K;
+          key[j] = entry_key(c, (int64_t)bh * NK + e, i, r);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (key[j] >= 0) visit(key[j], e0 + j * 1024 + tid);
+    }
+  };
+  walk([&](int key, int) { atomicAdd(&sc[key], 1); });
+  __syncthreads();
+  // exclusive scan: per-thread chunk sums, Hillis-Steele over the partials
+  const int per = (c.nkeys + 1023) / 1024;
+  const int k0 = tid * per, k1 = min(c.nkeys, k0 + per);
+  int sum = 0;
+  for (int k = k0; k < k1; ++k) sum += sc[k];
+  part[tid] = sum;
+  __syncthreads();
+  for (int d = 1; d < 1024; d <<= 1) {
+    const int x = tid >= d ? part[tid - d] : 0;
+    __syncthreads();
+    part[tid] += x;
+    __syncthreads();
+  }
+  int32_t* off = c.off + (int64_t)bh * (c.nkeys + 1);
+  int run = part[tid] - sum;
+  for (int k = k0; k < k1; ++k) {
+    const int n = sc[k];
+    off[k] = run;
+    sc[k] = run;                                   // fill cursor
+    run += n;
+  }
+  if (tid == 1023) off[c.nkeys] = part[1023];
+  __syncthreads();
+  int32_t* tmp = c.tmp + (int64_t)bh * NK;
+  walk([&](int key, int e) { tmp[atomicAdd(&sc[key], 1)] = e; });
+}
+
 // one wave per key: rank sort of the bucket (entry ids are distinct)
 constexpr int SORT_LDS = 1024;
 __global__ __launch_bounds__(256) void csr_sort_kernel(CsrArgs c) {
@@ -846,6 +905,13 @@ int launch_inv_map(const int32_t* cand, int Nq, int N, int32_t* inv, hipStream_t
 int launch_csr(const CsrArgs& c, hipStream_t s) {
   const int64_t ne = (int64_t)c.BH * c.N * c.K;
   if (ne <= 0 || c.nkeys <= 0) return 0;
+  if (c.nkeys <= CSR_LDS_MAX_KEYS && (int64_t)c.N * c.K <= INT32_MAX) {
+    hipLaunchKernelGGL(csr_lds_kernel, dim3(c.BH), dim3(1024), (size_t)(c.nkeys + 1024) * sizeof(int), s,
+                       c);
+    hipLaunchKernelGGL(csr_sort_kernel, dim3((unsigned)(((int64_t)c.BH * c.nkeys + 3) / 4)), dim3(256),
+                       0, s, c);
+    return (int)hipGetLastError();
+  }
   int st = launch_fill_i32(c.cnt, (int64_t)c.BH * c.nkeys, 0, s);
   if (st) return st;
   hipLaunchKernelGGL(csr_count_kernel, grid_for(ne), dim3(256), 0, s, c);

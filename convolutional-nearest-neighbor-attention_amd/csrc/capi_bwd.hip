@@ -15,7 +15,7 @@ using namespace cnna_desc_util;
 namespace {
 
 struct CorePlan {
-  void *dy, *t1, *dt1, *w0p, *dP, *dqkv, *dqs, *xs, *dxs;
+  void *dy, *t1, *dt1, *w0p, *dP, *dqkv, *dqs, *xs, *dxs, *wt;
   float *coef, *w0part, *part;
   int32_t *cnt, *off, *tmp, *list, *cnt2, *off2, *tmp2, *list2, *inv;
   size_t bytes;
@@ -46,6 +46,7 @@ CorePlan plan_core(const cnna_desc* d, void* ws) {
   if (d->conv != CNNA_CONV_STANDARD)
     p.w0part = static_cast<float*>(c.take((size_t)tok_bwd_blocks((int)BH, (int)N) * din * K * 4));
   p.dqkv = c.take(B * N * (d->sampled ? 2 : 3) * C * es);
+  p.wt = c.take(3 * C * C * es);                 // [W_q^T | W_k^T | W_v^T] for dx
   p.cnt = static_cast<int32_t*>(c.take(BH * N * 4));
   p.off = static_cast<int32_t*>(c.take(BH * (N + 1) * 4));
   p.tmp = static_cast<int32_t*>(c.take(ent * 4));
@@ -112,7 +113,8 @@ extern "C" {
 
 size_t cnna_output_proj_backward_workspace(const cnna_desc* d) {
   if (cnna_check_desc(d)) return 0;
-  return cnna_round_up(part_floats(d->dtype, d->C, d->C, d->B * d->N) * 4, 256);
+  return cnna_round_up(part_floats(d->dtype, d->C, d->C, d->B * d->N) * 4, 256) +
+         cnna_round_up((size_t)d->C * d->C * elem_size(d->dtype), 256);   // W_o^T
 }
 
 int cnna_output_proj_backward(const cnna_desc* d, const void* z, const void* Wo, const void* dout,
@@ -125,13 +127,23 @@ int cnna_output_proj_backward(const cnna_desc* d, const void* z, const void* Wo,
   if (ws_bytes < cnna_output_proj_backward_workspace(d)) return CNNA_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
   const int M = d->B * d->N, C = d->C;
-  // dz[m][c] = sum_n dout[m][n] Wo[n][c]
-  GradGemmArgs g = gg(M, C, C, dout, ld_dout, GG_ROWS, Wo, C, GG_TRANS);
-  g.o = dz;
-  g.ldo = C;
-  if ((st = launch_gemm_grad(d->dtype, g, s))) return st;
+  // dz[m][c] = sum_n dout[m][n] Wo[n][c]: a row GEMM against W_o^T (the forward kernel)
+  char* wtp = static_cast<char*>(ws) + cnna_round_up(part_floats(d->dtype, C, C, M) * 4, 256);
+  if ((st = launch_transpose(d->dtype, Wo, wtp, C, C, C, s))) return st;
+  {
+    const int es = elem_size(d->dtype);
+    GemmArgs f;
+    memset(&f, 0, sizeof(f));
+    f.M = M; f.Nc = C; f.Kd = C;
+    f.a = dout; f.lda = ld_dout;
+    f.avec = ((C * es) % 16 == 0) && ((ld_dout * es) % 16 == 0) && aligned16(dout);
+    f.w[0] = wtp; f.ncol_each = C;
+    f.bvec = ((C * es) % 16 == 0) && aligned16(wtp);
+    f.o[0] = dz; f.ldo = C;
+    if ((st = launch_gemm(d->dtype, GEMM_A_ROWS, GEMM_O_PLAIN, f, s))) return st;
+  }
   // dWo[n][c] = sum_m dout[m][n] z[m][c]
-  g = gg(C, C, M, dout, ld_dout, GG_TRANS, z, C, GG_TRANS);
+  GradGemmArgs g = gg(C, C, M, dout, ld_dout, GG_TRANS, z, C, GG_TRANS);
   return weight_grad(d->dtype, g, static_cast<float*>(ws), dWo, nullptr, nullptr, C, C, 0, 0, s);
 }
 
@@ -264,18 +276,30 @@ int cnna_core_backward(const cnna_desc* d, const void* x, int64_t ldx, const int
     if ((st = launch_pull(dt, pa, s))) return st;
   }
 
-  // 5. projections: dx and the weight gradients
-  GradGemmArgs g = gg(B * N, C, ld3, p.dqkv, ld3, GG_ROWS, nullptr, C, GG_TRANS);
-  g.w_krows = C;
-  if (d->sampled) {
-    g.w[0] = Wk; g.w[1] = Wv; g.w[2] = Wv;
-  } else {
-    g.w[0] = Wq; g.w[1] = Wk; g.w[2] = Wv;
+  // 5. projections: dx and the weight gradients.  dx = dqkv @ [W_q; W_k; W_v]
+  // as a row GEMM against the transposed stack (the forward kernel)
+  {
+    const void* ws3[3] = {Wq, Wk, Wv};
+    const void* ws2[2] = {Wk, Wv};
+    const int nm = d->sampled ? 2 : 3;
+    for (int j = 0; j < nm; ++j) {
+      const void* src = d->sampled ? ws2[j] : ws3[j];
+      if ((st = launch_transpose(dt, src, static_cast<char*>(p.wt) + (size_t)j * C * elem_size(dt), C, C,
+                                 ld3, s)))
+        return st;
+    }
+    const int es = elem_size(dt);
+    GemmArgs f;
+    memset(&f, 0, sizeof(f));
+    f.M = B * N; f.Nc = C; f.Kd = ld3;
+    f.a = p.dqkv; f.lda = ld3;
+    f.avec = ((ld3 * es) % 16 == 0) && aligned16(p.dqkv);
+    f.w[0] = p.wt; f.ncol_each = C;
+    f.bvec = ((ld3 * es) % 16 == 0) && aligned16(p.wt);
+    f.o[0] = gr->dx; f.ldo = C;
+    if ((st = launch_gemm(dt, GEMM_A_ROWS, GEMM_O_PLAIN, f, s))) return st;
   }
-  g.o = gr->dx;
-  g.ldo = C;
-  if ((st = launch_gemm_grad(dt, g, s))) return st;
-  g = gg(ld3, C, B * N, p.dqkv, ld3, GG_TRANS, x, ldx, GG_TRANS);
+  GradGemmArgs g = gg(ld3, C, B * N, p.dqkv, ld3, GG_TRANS, x, ldx, GG_TRANS);
   if (d->sampled) {
     if ((st = weight_grad(dt, g, p.part, gr->dWk, gr->dWv, nullptr, C, C, 0, 0, s))) return st;
     if (Nq > 0) {

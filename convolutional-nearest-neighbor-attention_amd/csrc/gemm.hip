@@ -476,7 +476,44 @@ __global__ void permute_w0t_kernel(const T* w0, T* w0t, int dout, int din, int K
   w0t[((int64_t)r * din + c) * dout + o] = w0[e];
 }
 
+// dst[c * ldd + k] = src[k * cols + c] for a (rows, cols) source: 32 x 32
+// tiles through LDS (many small blocks: the matrices are weights, a few MB),
+// reads and writes coalesced
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_kernel(const T* src, T* dst, int rows, int cols,
+                                                        int64_t ldd) {
+  __shared__ T tile[32][33];
+  const int k0 = blockIdx.x * 32, c0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+#pragma unroll
+  for (int r = ty; r < 32; r += 8) {
+    const int k = k0 + r, c = c0 + tx;
+    if (k < rows && c < cols) tile[r][tx] = src[(int64_t)k * cols + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = ty; r < 32; r += 8) {
+    const int c = c0 + r, k = k0 + tx;
+    if (k < rows && c < cols) dst[(int64_t)c * ldd + k] = tile[tx][r];
+  }
+}
+
 }  // namespace
+
+int launch_transpose(int dtype, const void* src, void* dst, int rows, int cols, int64_t ldd,
+                     hipStream_t s) {
+  if (rows <= 0 || cols <= 0) return 0;
+  const dim3 grid((unsigned)((rows + 31) / 32), (unsigned)((cols + 31) / 32));
+  if (dtype == CNNA_BF16)
+    hipLaunchKernelGGL(transpose_kernel<uint16_t>, grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), rows, cols, ldd);
+  else if (dtype == CNNA_F32)
+    hipLaunchKernelGGL(transpose_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(src),
+                       static_cast<float*>(dst), rows, cols, ldd);
+  else
+    return CNNA_ERR_DTYPE;
+  return (int)hipGetLastError();
+}
 
 int launch_permute_w0t(int dtype, const void* w0, void* w0t, int dout, int din, int K, hipStream_t s) {
   const int64_t total = (int64_t)dout * din * K;

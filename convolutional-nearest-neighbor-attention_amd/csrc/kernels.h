@@ -117,6 +117,10 @@ int launch_aggregate(int dtype, const AggArgs& a, hipStream_t s);
 int launch_merge(int dtype, const AggArgs& a, hipStream_t s);
 // W0 (dout, din, K) -> W0p (dout, K*din) with W0p[o][r*din + c] = W0[o][c][r]
 int launch_permute_w0(int dtype, const void* w0, void* w0p, int dout, int din, int K, hipStream_t s);
+// dst[c * ldd + k] = src[k * cols + c]: transpose of a (rows, cols) matrix into
+// columns [0, rows) of a (cols, ldd) destination
+int launch_transpose(int dtype, const void* src, void* dst, int rows, int cols, int64_t ldd,
+                     hipStream_t s);
 // W0 (dout, din, K) -> W0t (K*din, dout), W0t[r*din + c][o] = W0[o][c][r]
 int launch_permute_w0t(int dtype, const void* w0, void* w0t, int dout, int din, int K, hipStream_t s);
 
