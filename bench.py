@@ -225,14 +225,19 @@ def run_vit(args):
     ts = []
     with torch.no_grad():
         q, k, v, qn, kn = ops.project_qkv(d, x, None, blk.W_q.weight, blk.W_k.weight, blk.W_v.weight)
+        # back to back, one synchronisation at the end: the host runs ahead of the
+        # GPU, so each event pair brackets the kernel alone (a synchronisation per
+        # launch would add the host's launch latency to every interval)
+        evs = []
         for it in range(args.warmup + args.steps):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             ops.select(d, k, q, kn, qn, None)
             e1.record()
             if it >= args.warmup:
-                torch.cuda.synchronize()
-                ts.append(e0.elapsed_time(e1))
+                evs.append((e0, e1))
+        torch.cuda.synchronize()
+        ts = [e0.elapsed_time(e1) for e0, e1 in evs]
     t_sel = sorted(ts)[len(ts) // 2] / 1e3
     f_sim = 2 * B * 197 * 197 * 192
     achieved = f_sim / t_sel / 1e12
@@ -327,14 +332,19 @@ def run_callers(args):
     ts = []
     with torch.no_grad():
         q, k, v, qn, kn = ops.project_qkv(d, x[:, :, :C1], None, Wq, Wk, Wv)
+        # back to back, one synchronisation at the end: the host runs ahead of the
+        # GPU, so each event pair brackets the kernel alone (a synchronisation per
+        # launch would add the host's launch latency to every interval)
+        evs = []
         for it in range(args.warmup + args.steps):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             ops.select(d, k, q, kn, qn, None)
             e1.record()
             if it >= args.warmup:
-                torch.cuda.synchronize()
-                ts.append(e0.elapsed_time(e1))
+                evs.append((e0, e1))
+        torch.cuda.synchronize()
+        ts = [e0.elapsed_time(e1) for e0, e1 in evs]
     t_sel = sorted(ts)[len(ts) // 2] / 1e3
     f_sim = 2 * B * N * N * C1
     achieved = f_sim / t_sel / 1e12
@@ -450,6 +460,8 @@ def main():
     Wq, Wk, Wv, Wo = m.W_q.weight, m.W_k.weight, m.W_v.weight, m.W_o.weight
     stages = {"project": [], "select": [], "aggregate": [], "output_proj": []}
     with torch.no_grad():
+        # back to back, one synchronisation at the end (see run_vit)
+        evl = []
         for it in range(args.warmup + args.steps):
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
             ev[0].record()
@@ -462,9 +474,11 @@ def main():
             ops.output_proj(d, z, Wo)
             ev[4].record()
             if it >= args.warmup:
-                torch.cuda.synchronize()
-                for i, name in enumerate(stages):
-                    stages[name].append(ev[i].elapsed_time(ev[i + 1]))
+                evl.append(ev)
+        torch.cuda.synchronize()
+        for ev in evl:
+            for i, name in enumerate(stages):
+                stages[name].append(ev[i].elapsed_time(ev[i + 1]))
     st_ms = {k_: sorted(v_)[len(v_) // 2] for k_, v_ in stages.items()}
 
     proj_f, sim_f, conv_f = flops_of(B, N, Nq, C, H, K, conv)
