@@ -128,3 +128,36 @@ def test_autocast_runs_bf16_and_reaches_fp32_weights():
     # (the bfloat16 layer's own parity is covered by the bf16 parity tests; it
     # is not compared with the float32 layer here: bf16 rounding of q and k
     # flips near-tied neighbour choices, which moves whole rows)
+
+
+@pytest.mark.parametrize("layer", ["ConvNNAttention", "KvtAttention"])
+def test_forward_replays_from_a_hip_graph(layer):
+    # the inference forward launches no memset and allocates nothing inside the
+    # library, so it can be captured; every replay (with eager work and
+    # synchronisations between replays) equals the eager forward
+    torch.manual_seed(0)
+    args = vit_tiny_args(layer=layer, img_size=(3, 64, 64), patch_size=8, num_layers=2, dropout=0.0,
+                         attention_dropout=0.0)
+    model = ViT(args).to(DEV).to(torch.bfloat16).eval()
+    for blk in model.transformer_encoder:
+        if hasattr(blk.attention, "seq_length"):
+            blk.attention.seq_length = 65
+    imgs = torch.randn(8, 3, 64, 64, device=DEV).to(torch.bfloat16)
+    static_in = imgs.clone()
+    with torch.no_grad():
+        ref = model(imgs)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                model(static_in)
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            static_out = model(static_in)
+        for _ in range(4):
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(static_out, ref)
+            model(torch.randn_like(imgs))          # eager work between replays
+            torch.cuda.synchronize()
