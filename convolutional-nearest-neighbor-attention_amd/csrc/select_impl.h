@@ -324,7 +324,10 @@ void select_kernel(SelArgs a) {
     float L[KMAX];
     // Short rows (at most 16 tiles): groups of 4 candidates, so that tau is
     // drawn from enough groups to sit close to the K-th key (fewer passers
-    // and queue drains in pass 2); long rows: groups of 16.
+    // and queue drains in pass 2); long rows: groups of 16.  Long lists on
+    // very short rows (K >= 16, at most 8 tiles): every candidate is inserted,
+    // tau is the exact K-th key and only about K candidates reach the queues.
+    const bool every = KMAX >= 16 && ntiles <= 8;
     const bool fine = ntiles <= 16;
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) L[r] = -INFINITY;
@@ -341,7 +344,10 @@ void select_kernel(SelArgs a) {
           if (decltype(MASKED)::value && j0 + jl >= a.Nq) key[v] = -INFINITY;
         }
         // keys here are finite or -inf (masked rows, negative euclidean d^2)
-        if (fine) {
+        if (every) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) bound_insert<KMAX>(L, key[v]);
+        } else if (fine) {
 #pragma unroll
           for (int g = 0; g < 4; ++g)
             bound_insert<KMAX>(L, max2(max2(key[4 * g], key[4 * g + 1]), max2(key[4 * g + 2], key[4 * g + 3])));
