@@ -378,20 +378,36 @@ int launch_tok_c(const TokBwdArgs& a, hipStream_t s) {
   return CNNA_ERR_SHAPE;
 }
 
-__global__ __launch_bounds__(256) void w0_reduce_f32(const float* part, int nblk, int n, float* out) {
-  const int e = blockIdx.x * 256 + threadIdx.x;
-  if (e >= n) return;
+// Sum of the per-block depthwise-weight partials: a block owns 32 outputs; 32
+// thread groups each add every 32nd partial (four loads in flight), then the
+// group sums are added in group order.  Fixed order: deterministic.
+template <typename T>
+__global__ __launch_bounds__(1024) void w0_reduce_kernel(const float* part, int nblk, int n, T* out) {
+  __shared__ float red[32][33];
+  const int el = threadIdx.x & 31, gb = threadIdx.x >> 5;
+  const int e = blockIdx.x * 32 + el;
   float acc = 0.0f;
-  for (int b = 0; b < nblk; ++b) acc += part[(int64_t)b * n + e];
-  out[e] = acc;
-}
-__global__ __launch_bounds__(256) void w0_reduce_bf16(const float* part, int nblk, int n,
-                                                      uint16_t* out) {
-  const int e = blockIdx.x * 256 + threadIdx.x;
-  if (e >= n) return;
-  float acc = 0.0f;
-  for (int b = 0; b < nblk; ++b) acc += part[(int64_t)b * n + e];
-  out[e] = f2bf(acc);
+  if (e < n) {
+    int b = gb;
+    for (; b + 96 < nblk; b += 128) {
+      const float v0 = part[(int64_t)b * n + e];
+      const float v1 = part[(int64_t)(b + 32) * n + e];
+      const float v2 = part[(int64_t)(b + 64) * n + e];
+      const float v3 = part[(int64_t)(b + 96) * n + e];
+      acc += v0;
+      acc += v1;
+      acc += v2;
+      acc += v3;
+    }
+    for (; b < nblk; b += 32) acc += part[(int64_t)b * n + e];
+  }
+  red[gb][el] = acc;
+  __syncthreads();
+  if (gb == 0 && e < n) {
+    float sum = 0.0f;
+    for (int g = 0; g < 32; ++g) sum += red[g][el];
+    stf(out + e, sum);
+  }
 }
 
 // ------------------------------------------------------------------ CSR
@@ -878,11 +894,12 @@ int launch_tok_bwd(int dtype, const TokBwdArgs& a0, hipStream_t s) {
 
 int launch_w0_reduce(int dtype, const float* part, int nblk, int n, void* out, hipStream_t s) {
   if (n <= 0) return 0;
+  const dim3 grid((unsigned)((n + 31) / 32));
   if (dtype == CNNA_BF16)
-    hipLaunchKernelGGL(w0_reduce_bf16, grid_for(n), dim3(256), 0, s, part, nblk, n,
+    hipLaunchKernelGGL(w0_reduce_kernel<uint16_t>, grid, dim3(1024), 0, s, part, nblk, n,
                        static_cast<uint16_t*>(out));
   else if (dtype == CNNA_F32)
-    hipLaunchKernelGGL(w0_reduce_f32, grid_for(n), dim3(256), 0, s, part, nblk, n,
+    hipLaunchKernelGGL(w0_reduce_kernel<float>, grid, dim3(1024), 0, s, part, nblk, n,
                        static_cast<float*>(out));
   else
     return CNNA_ERR_DTYPE;
