@@ -158,9 +158,28 @@ CNNA_DEV float row16_sum(float v) {
   return v;
 }
 
-template <typename T, int CPL, int KMAX, bool DW>
+// sum over groups of N lanes (N = 8 or 16) inside a DPP row
+template <int N>
+CNNA_DEV float rowN_sum(float v) {
+  v += dpp_f<0xB1>(v);                    // quad_perm [1, 0, 3, 2]
+  v += dpp_f<0x4E>(v);                    // quad_perm [2, 3, 0, 1]
+  v += dpp_f<0x141>(v);                   // row_half_mirror: the two quads of 8 lanes
+  if (N == 16) v += dpp_f<0x140>(v);      // row_mirror: the two halves of 16 lanes
+  return v;
+}
+
+// DV (depthwise, din a multiple of the 16-byte vector): the neighbour-weight
+// gradients use LPR = 64*CPL/V16 lanes per neighbour row with 16-byte loads of
+// v and g, 64/LPR neighbours per pass and DPP sums over the LPR lanes; the
+// depthwise-weight partials accumulate in that layout.
+template <typename T, int CPL, int KMAX, bool DW, bool DV = false>
 __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
   constexpr int CW = 64 * CPL;
+  constexpr int V16 = 16 / sizeof(T);
+  constexpr int LPR = CW / V16 > 0 ? CW / V16 : 1;   // lanes per neighbour row (DV)
+  constexpr int RPP = 64 / LPR;                        // neighbours per pass (DV)
+  constexpr int NPS = (KMAX + RPP - 1) / RPP;          // passes (DV)
+  static_assert(!DV || (DW && (LPR == 8 || LPR == 16)), "DV needs 8 or 16 lanes per row");
   __shared__ float sW[DW ? KMAX * CW : 1];   // W0 as [r][c]; reused for the block reduction
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int c0 = lane * CPL;
@@ -173,11 +192,17 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
     }
     __syncthreads();
   }
-  float acc[DW ? KMAX : 1][CPL];
+  float acc[(DW && !DV) ? KMAX : 1][CPL];
 #pragma unroll
-  for (int r = 0; r < (DW ? KMAX : 1); ++r)
+  for (int r = 0; r < ((DW && !DV) ? KMAX : 1); ++r)
 #pragma unroll
     for (int u = 0; u < CPL; ++u) acc[r][u] = 0.0f;
+  float accd[DV ? NPS : 1][DV ? V16 : 1];
+#pragma unroll
+  for (int p = 0; p < (DV ? NPS : 1); ++p)
+#pragma unroll
+    for (int u = 0; u < (DV ? V16 : 1); ++u) accd[p][u] = 0.0f;
+  const int dgrp = lane / LPR, dgl = lane % LPR, dc = dgl * V16;   // DV lane layout
 
   const bool euc = a.metric == CNNA_EUCLIDEAN, cos_ = a.metric == CNNA_COSINE;
   const bool gvec = (a.din % CPL) == 0;
@@ -200,10 +225,48 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
     const float my_wa = my_w * my_mul;   // the weight the aggregation used
     const T* V = static_cast<const T*>(a.v) + (int64_t)bh * a.N * a.dkp;
     float gv[CPL];
-    if (DW) load_row<T, CPL>(static_cast<const T*>(a.g) + (int64_t)tok * a.din, c0, a.din, gvec, gv);
+    if (DW && !DV) load_row<T, CPL>(static_cast<const T*>(a.g) + (int64_t)tok * a.din, c0, a.din, gvec, gv);
 
     // dw[r] = sum_c dP[c, r] * v[c, idx[r]]
     float my_dw = 0.0f;
+    if constexpr (DV) {
+      const bool cok = dc < a.din;
+      float gq[V16];
+      if (cok) {
+        Row<T, V16>::load(static_cast<const T*>(a.g) + (int64_t)tok * a.din + dc, gq);
+      } else {
+#pragma unroll
+        for (int u = 0; u < V16; ++u) gq[u] = 0.0f;
+      }
+#pragma unroll
+      for (int ps = 0; ps < NPS; ++ps) {
+        const int r0 = ps * RPP;
+        if (r0 < K) {
+          const int r = r0 + dgrp;
+          const int rr = min(r, K - 1);
+          const int t = __shfl(my_j, rr);
+          const float wr = __shfl(my_wa, rr);
+          float p = 0.0f;
+          if (cok) {
+            float vv[V16];
+            Row<T, V16>::load(V + (int64_t)t * a.dkp + dc, vv);
+            const bool rok = r < K;
+#pragma unroll
+            for (int u = 0; u < V16; ++u) {
+              const float pr = gq[u] * vv[u];
+              if (rok) accd[ps][u] += wr * pr;
+              p += sW[rr * CW + dc + u] * pr;
+            }
+          }
+          p = rowN_sum<LPR>(p);
+#pragma unroll
+          for (int q = 0; q < RPP; ++q) {
+            const float sq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), q * LPR));
+            if (lane == r0 + q) my_dw = sq;
+          }
+        }
+      }
+    }
     if (!DW && svec) {
       // standard conv: four neighbours per pass, 16 lanes per neighbour row
       // with 16-byte loads of dP and v, row sums by DPP inside the 16 lanes
@@ -240,7 +303,7 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
     }
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) {
-      if (r < K && (DW || !svec)) {
+      if (r < K && ((DW && !DV) || (!DW && !svec))) {
         const int t = __builtin_amdgcn_readlane(my_j, r);
         float vv[CPL];
         load_row<T, CPL>(V + (int64_t)t * a.dkp, c0, a.dkp, true, vv);
@@ -335,13 +398,28 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
     __syncthreads();
     for (int w = 0; w < 4; ++w) {
       if (wv == w) {
+        if constexpr (DV) {
+          // every wave covers the same (r < K, c < din) entries
 #pragma unroll
-        for (int r = 0; r < KMAX; ++r)
+          for (int ps = 0; ps < NPS; ++ps) {
+            const int r = ps * RPP + dgrp;
+            if (r < K && dc < a.din) {
 #pragma unroll
-          for (int u = 0; u < CPL; ++u) {
-            float* p = &sW[(DW ? r : 0) * CW + c0 + u];
-            *p = (w == 0 ? 0.0f : *p) + acc[DW ? r : 0][u];
+              for (int u = 0; u < V16; ++u) {
+                float* p = &sW[r * CW + dc + u];
+                *p = (w == 0 ? 0.0f : *p) + accd[ps][u];
+              }
+            }
           }
+        } else {
+#pragma unroll
+          for (int r = 0; r < KMAX; ++r)
+#pragma unroll
+            for (int u = 0; u < CPL; ++u) {
+              float* p = &sW[(DW ? r : 0) * CW + c0 + u];
+              *p = (w == 0 ? 0.0f : *p) + acc[(DW && !DV) ? r : 0][u];
+            }
+        }
       }
       __syncthreads();
     }
@@ -356,10 +434,17 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
 template <typename T, int CPL, int KMAX>
 int launch_tok_t(const TokBwdArgs& a, hipStream_t s) {
   dim3 grid(a.nblk);
+  constexpr int LPR = 64 * CPL / (16 / (int)sizeof(T));
   if (a.std_conv)
     hipLaunchKernelGGL((tok_bwd_kernel<T, CPL, KMAX, false>), grid, dim3(256), 0, s, a);
-  else
+  else if constexpr (LPR == 8 || LPR == 16) {
+    if (a.din % (16 / (int)sizeof(T)) == 0)
+      hipLaunchKernelGGL((tok_bwd_kernel<T, CPL, KMAX, true, true>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((tok_bwd_kernel<T, CPL, KMAX, true>), grid, dim3(256), 0, s, a);
+  } else {
     hipLaunchKernelGGL((tok_bwd_kernel<T, CPL, KMAX, true>), grid, dim3(256), 0, s, a);
+  }
   return (int)hipGetLastError();
 }
 
