@@ -749,18 +749,26 @@ __global__ __launch_bounds__(256) void pull_kernel(PullArgs a) {
   }
 }
 
-// Same sums with four keys per wave: a 16-lane group owns one key and walks
-// its entries in list order with 16-byte row loads (NP passes of 16 * V16
-// channels); the cosine row dot product is a DPP row sum.  Rows of dP / g and
+template <typename T, int CPL>
+constexpr int pull_lanes_per_key() {
+  return (64 * CPL) / (16 / (int)sizeof(T)) <= 8 ? 8 : 16;
+}
+
+// Same sums with four (or eight) keys per wave: a group of 16 (or 8, when a
+// row is 8 vectors) lanes owns one key and walks its entries in list order
+// with 16-byte row loads (NP passes of LPK * V16 channels); the cosine row dot
+// product is a DPP sum over the group.  Rows of dP / g and
 // k must be whole 16-byte vectors (din % V16 == 0).
 template <typename T, int CPL>
 __global__ __launch_bounds__(256) void pull16_kernel(PullArgs a) {
   constexpr int V16 = 16 / sizeof(T);
-  constexpr int NP = (64 * CPL + 16 * V16 - 1) / (16 * V16);
   constexpr int CW = 64 * CPL;
+  constexpr int LPK = pull_lanes_per_key<T, CPL>();   // 8 when a row is 8 vectors, else 16
+  constexpr int KPW = 64 / LPK;                       // keys per wave
+  constexpr int NP = (CW + LPK * V16 - 1) / (LPK * V16);
   extern __shared__ float sW[];                   // depthwise: W0 as [r][c]
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int grp = lane >> 4, gl = lane & 15;
+  const int grp = lane / LPK, gl = lane % LPK;
   const bool dwv = a.do_v && !a.std_conv;
   if (dwv) {
     const T* W0 = static_cast<const T*>(a.w0);
@@ -771,7 +779,7 @@ __global__ __launch_bounds__(256) void pull16_kernel(PullArgs a) {
     __syncthreads();
   }
   const int64_t nk = (int64_t)a.BH * a.nkeys;
-  const int64_t gk = ((int64_t)blockIdx.x * 4 + wv) * 4 + grp;
+  const int64_t gk = ((int64_t)blockIdx.x * 4 + wv) * KPW + grp;
   const bool kvalid = gk < nk;
   const int64_t gkc = kvalid ? gk : nk - 1;      // idle groups walk a real key, store nothing
   const int bh = (int)(gkc / a.nkeys), key = (int)(gkc - (int64_t)bh * a.nkeys);
@@ -797,7 +805,7 @@ __global__ __launch_bounds__(256) void pull16_kernel(PullArgs a) {
       const T* row = a.std_conv ? DP + (bh * NK + e) * a.din : G + ((int64_t)bh * a.N + i) * a.din;
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
-        const int c = (p * 16 + gl) * V16;
+        const int c = (p * LPK + gl) * V16;
         if (c < a.din) {
           float gg[V16];
           Row<T, V16>::load(row + c, gg);
@@ -816,7 +824,7 @@ __global__ __launch_bounds__(256) void pull16_kernel(PullArgs a) {
       if (ce != 0.0f) {
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-          const int c = (p * 16 + gl) * V16;
+          const int c = (p * LPK + gl) * V16;
           if (c < a.dkp) {
             float kk[V16];
             Row<T, V16>::load(Kt + (int64_t)i * a.dkp + c, kk);
@@ -834,7 +842,7 @@ __global__ __launch_bounds__(256) void pull16_kernel(PullArgs a) {
     for (int p = 0; p < NP; ++p)
 #pragma unroll
       for (int u = 0; u < V16; ++u) {
-        const int c = (p * 16 + gl) * V16 + u;
+        const int c = (p * LPK + gl) * V16 + u;
         if (c < a.dk) stf(dst + c, dv[p][u]);
       }
   }
@@ -845,7 +853,7 @@ __global__ __launch_bounds__(256) void pull16_kernel(PullArgs a) {
       float d = 0.0f;
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
-        const int c = (p * 16 + gl) * V16;
+        const int c = (p * LPK + gl) * V16;
         if (c < a.dkp) {
           Row<T, V16>::load(qrow + c, qv[p]);
         } else {
@@ -856,7 +864,7 @@ __global__ __launch_bounds__(256) void pull16_kernel(PullArgs a) {
         for (int u = 0; u < V16; ++u) d += qv[p][u] * dq[p][u];
       }
       if (a.metric == CNNA_COSINE) {
-        d = row16_sum(d);
+        d = rowN_sum<LPK>(d);
         const float nrm = sqrtf(a.qn[(int64_t)bh * a.nkeys + key]);
 #pragma unroll
         for (int p = 0; p < NP; ++p)
@@ -877,7 +885,7 @@ __global__ __launch_bounds__(256) void pull16_kernel(PullArgs a) {
       for (int p = 0; p < NP; ++p)
 #pragma unroll
         for (int u = 0; u < V16; ++u) {
-          const int c = (p * 16 + gl) * V16 + u;
+          const int c = (p * LPK + gl) * V16 + u;
           if (c < a.dk) stf(dst + c, dq[p][u]);
         }
     }
@@ -892,13 +900,17 @@ int launch_pull_t(const PullArgs& a, hipStream_t s) {
   auto lds = [&](int cpl) { return (size_t)((a.do_v && !a.std_conv) ? a.K * 64 * cpl * 4 : 0); };
   constexpr int V16 = 16 / sizeof(T);
   if (a.din % V16 == 0 && a.dkp <= 256) {
-    const dim3 grid16((unsigned)((waves + 15) / 16));
+    auto g16 = [&](int cpl) {
+      const int kpw = 64 / (cpl == 1 ? pull_lanes_per_key<T, 1>()
+                                     : (cpl == 2 ? pull_lanes_per_key<T, 2>() : pull_lanes_per_key<T, 4>()));
+      return dim3((unsigned)((waves + 4 * kpw - 1) / (4 * kpw)));
+    };
     if (a.dkp <= 64)
-      hipLaunchKernelGGL((pull16_kernel<T, 1>), grid16, dim3(256), lds(1), s, a);
+      hipLaunchKernelGGL((pull16_kernel<T, 1>), g16(1), dim3(256), lds(1), s, a);
     else if (a.dkp <= 128)
-      hipLaunchKernelGGL((pull16_kernel<T, 2>), grid16, dim3(256), lds(2), s, a);
+      hipLaunchKernelGGL((pull16_kernel<T, 2>), g16(2), dim3(256), lds(2), s, a);
     else
-      hipLaunchKernelGGL((pull16_kernel<T, 4>), grid16, dim3(256), lds(4), s, a);
+      hipLaunchKernelGGL((pull16_kernel<T, 4>), g16(4), dim3(256), lds(4), s, a);
     return (int)hipGetLastError();
   }
   if (a.dkp <= 64)
