@@ -101,6 +101,8 @@ BWD_EXTRA = [
     ("spatial_dup_columns", dict(d_hidden=48, num_heads=3, K=5, sampling_type="spatial", num_samples=40, seq_length=24), 2, 24),
     ("k32_dk128", dict(d_hidden=256, num_heads=2, K=32, seq_length=80), 2, 80),
     ("dk128_std_k16", dict(d_hidden=256, num_heads=2, K=16, convolution_type="standard", seq_length=64), 1, 64),
+    # depthwise with 20-channel heads: the vector weight-gradient path (fp32, 5 vectors per row)
+    ("matmul_dw_dk20", dict(d_hidden=60, num_heads=3, K=7, seq_length=45), 2, 45),
 ]
 
 
@@ -110,9 +112,12 @@ def test_backward_fp32_more(name, kw, B, N):
 
 
 @pytest.mark.parametrize("conv,N,C,K", [("standard", 512, 768, 16), ("depthwise", 1024, 384, 9),
-                                        ("depthwise", 256, 768, 32)])
+                                        ("depthwise", 256, 768, 32), ("depthwise", 197, 192, 9),
+                                        ("depthwise", 64, 60, 7)])
 def test_backward_bf16(conv, N, C, K):
-    """bf16 at config-5 / config-3 head sizes (batch reduced)."""
+    """bf16 at config-5 / config-3 / ViT head sizes (batch reduced); 20-channel
+    heads take the element-wise weight-gradient path (rows not whole 16-byte
+    vectors)."""
     cfg = O.Config(d_hidden=C, num_heads=3, K=K, convolution_type=conv, seq_length=N)
     B = 2
     p, x = make(cfg, B, N, torch.bfloat16, seed=11)
