@@ -253,7 +253,7 @@ def run_vit(args):
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: images ~ N(0,1), random-init weights (seed 0)",
         "config": {"workload": "c2: ViT-Tiny forward, 12 ConvNN-Attention blocks (matmul, depthwise, "
-                               "K=9, sampling all, softmax_topk_val=False as the CLI default), "
+                               "K=9, sampling all, softmax_topk_val=True as main.py:48-49 forces), "
                                "B=128 images 224x224, patch 16",
                    "B": B, "N": 197, "C": 192, "H": 3, "K": 9, "layers": 12},
         "roofline": {"kernel": "select", "bound": "mfma", "achieved": round(achieved, 2),
@@ -297,7 +297,7 @@ def run_callers(args):
     else:
         m = MultiHeadBranchingConv(C, H, 0.0, kernel_size=9, K=K, sampling_type="all", num_samples=-1,
                                    sample_padding=0, magnitude_type=metric, seq_length=N,
-                                   convolution_type=conv, softmax_topk_val=False, branch_ratio=0.5)
+                                   convolution_type=conv, softmax_topk_val=True, branch_ratio=0.5)
         C1 = m.d_hidden_convnn
     m = m.to("cuda").to(dtype).eval()
     x = torch.randn(B, N, C, device="cuda").to(dtype)
@@ -326,7 +326,7 @@ def run_callers(args):
         W = m.qkv.weight
         Wq, Wk, Wv = W[C:2 * C], W[:C], W[2 * C:]
     else:
-        d = ops.make_desc(B, N, C1, H, N, K, N, dtype, metric, conv, False, False, False)
+        d = ops.make_desc(B, N, C1, H, N, K, N, dtype, metric, conv, True, False, False)
         cv = m.convnn
         Wq, Wk, Wv = cv.W_q.weight, cv.W_k.weight, cv.W_v.weight
     ts = []
@@ -362,7 +362,7 @@ def run_callers(args):
             mc = __import__("copy").deepcopy(m).float().cpu()
             cv = mc.convnn
             cfg = O.Config(d_hidden=C1, num_heads=H, K=K, magnitude_type=metric, seq_length=N,
-                           convolution_type=conv, softmax_topk_val=False)
+                           convolution_type=conv, softmax_topk_val=True)
             p = O.Params(cv.W_q.weight, cv.W_k.weight, cv.W_v.weight, cv.W_o.weight, cv.conv.weight)
             c1 = mc.conv1d
             fn = lambda: O.branching_conv(

@@ -23,8 +23,8 @@ METRICS = {"matmul": 0, "cosine": 1, "euclidean": 2}
 CONVS = {"standard": 0, "depthwise": 1, "depthwise-separable": 2}
 MERGE_REFERENCE, MERGE_CONCAT = 0, 1
 
-ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_OPTION, ERR_K_RANGE, ERR_SEQ, ERR_WS, ERR_GROUPS = (
-    -1, -2, -3, -4, -5, -6, -7, -8)
+ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_OPTION, ERR_K_RANGE, ERR_SEQ, ERR_WS, ERR_GROUPS, ERR_UNSUPPORTED = (
+    -1, -2, -3, -4, -5, -6, -7, -8, -9)
 
 
 class Desc(ctypes.Structure):
@@ -38,7 +38,8 @@ class Desc(ctypes.Structure):
 class Saved(ctypes.Structure):
     """Mirror of ``cnna_saved``."""
 
-    _fields_ = [(n, ctypes.c_void_p) for n in ("q", "k", "v", "qn", "kn", "idx", "vals", "w", "wmul")]
+    _fields_ = [(n, ctypes.c_void_p) for n in ("q", "k", "v", "qn", "kn", "idx", "vals", "w", "wmul",
+                                               "cols")]
 
 
 class Grads(ctypes.Structure):
@@ -61,7 +62,7 @@ def _load():
         "cnna_check_desc": ([D], I32),
         "cnna_head_stride": ([D], I32),
         "cnna_project_qkv": ([D, P, I64, P, P, P, P, P, P, P, P, P, P], I32),
-        "cnna_select": ([D, P, P, P, P, P, P, P, P, P], I32),
+        "cnna_select": ([D, P, P, P, P, P, P, P, P, P, P], I32),
         "cnna_aggregate_workspace": ([D], ctypes.c_size_t),
         "cnna_aggregate": ([D, P, P, P, P, P, P, P, ctypes.c_size_t, P], I32),
         "cnna_output_proj": ([D, P, P, P, I64, P], I32),
@@ -84,7 +85,7 @@ def _load():
     return lib
 
 
-ABI_VERSION = 2        # CNNA_ABI_VERSION of the include/cnna.h this binding mirrors
+ABI_VERSION = 3        # CNNA_ABI_VERSION of the include/cnna.h this binding mirrors
 LIB = _load()
 if LIB.cnna_abi_version() != ABI_VERSION:
     raise ImportError(f"libcnna.so ABI {LIB.cnna_abi_version()} != {ABI_VERSION}: rebuild it with "
@@ -109,6 +110,9 @@ def check(status: int) -> None:
         raise ValueError(msg)
     if status in (ERR_DTYPE,):
         raise TypeError(msg)
+    if status == ERR_UNSUPPORTED:
+        # a configuration the reference runs but this build's kernels do not
+        raise NotImplementedError(msg)
     raise RuntimeError(msg)
 
 
@@ -180,13 +184,20 @@ def project_qkv(d: Desc, x: torch.Tensor, cand: Optional[torch.Tensor], Wq, Wk, 
 
 def select(d: Desc, k, q, kn=None, qn=None, cand=None):
     """Fused similarity + top-k: idx int32, vals fp32, neighbour weights fp32, all (BH,N,K)."""
+    return select_cols(d, k, q, kn, qn, cand)[:3]
+
+
+def select_cols(d: Desc, k, q, kn=None, qn=None, cand=None):
+    """``select`` plus, for sampled paths, the candidate column of each entry
+    (int32 (BH,N,K), slot 0 = Nq); cols is None for sampling 'all'."""
     BH = d.B * d.H
     idx = torch.empty((BH, d.N, d.K), dtype=torch.int32, device=k.device)
     vals = torch.empty((BH, d.N, d.K), dtype=torch.float32, device=k.device)
     w = torch.empty((BH, d.N, d.K), dtype=torch.float32, device=k.device)
+    cols = torch.empty((BH, d.N, d.K), dtype=torch.int32, device=k.device) if d.sampled else None
     check(LIB.cnna_select(ctypes.byref(d), _ptr(k), _ptr(q), _ptr(kn), _ptr(qn), _ptr(cand),
-                          _ptr(idx), _ptr(vals), _ptr(w), _stream()))
-    return idx, vals, w
+                          _ptr(idx), _ptr(vals), _ptr(w), _ptr(cols), _stream()))
+    return idx, vals, w, cols
 
 
 def aggregate(d: Desc, v, idx, w, w0, w1=None):
@@ -291,8 +302,10 @@ def conv1d_branch(x, Wx, bx, conv_w, conv_b, Wo, bo, num_heads, out=None):
 def output_proj_backward(d: Desc, z, Wo, dout):
     """dz = dout @ Wo, dWo = dout^T @ z."""
     dout = dout.contiguous()
-    dz = torch.empty_like(z)
-    dWo = torch.empty_like(Wo)
+    # row-major outputs whatever the strides of z / Wo (empty_like would keep
+    # a permuted layout, which the kernels do not write)
+    dz = torch.empty(z.shape, dtype=z.dtype, device=z.device)
+    dWo = torch.empty(Wo.shape, dtype=Wo.dtype, device=Wo.device)
     nws = LIB.cnna_output_proj_backward_workspace(ctypes.byref(d))
     ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=z.device)
     check(LIB.cnna_output_proj_backward(ctypes.byref(d), _ptr(z.contiguous()), _ptr(Wo.contiguous()),
@@ -304,10 +317,11 @@ def output_proj_backward(d: Desc, z, Wo, dout):
 def core_backward(d: Desc, x, cand, Wq, Wk, Wv, w0, w1, saved, dz):
     """Gradients of x, W_q, W_k, W_v and the conv weights from dz (B, N, C).
 
-    ``saved`` = (q, k, v, qn, kn, idx, vals, w, wmul) from the forward stages
-    (wmul: the multipliers applied to w before the aggregation, or None).
+    ``saved`` = (q, k, v, qn, kn, idx, vals, w, wmul, cols) from the forward
+    stages (wmul: the multipliers applied to w before the aggregation, or None;
+    cols: the sampled paths' candidate columns from ``select_cols``).
     """
-    q, k, v, qn, kn, idx, vals, w, wmul = saved
+    q, k, v, qn, kn, idx, vals, w, wmul, cols = saved
     x = _token_rows(x)
     dz = dz.contiguous()
     w0c = w0.to(x.dtype).contiguous()
@@ -316,7 +330,7 @@ def core_backward(d: Desc, x, cand, Wq, Wk, Wv, w0, w1, saved, dz):
     dWq, dWk, dWv = (torch.empty(W.shape, dtype=x.dtype, device=x.device) for W in (Wq, Wk, Wv))
     dw0 = torch.empty(w0.shape, dtype=x.dtype, device=x.device)
     dw1 = None if w1 is None else torch.empty(w1.shape, dtype=x.dtype, device=x.device)
-    sv = Saved(*(None if t is None else t.data_ptr() for t in (q, k, v, qn, kn, idx, vals, w, wmul)))
+    sv = Saved(*(None if t is None else t.data_ptr() for t in (q, k, v, qn, kn, idx, vals, w, wmul, cols)))
     gr = Grads(*(None if t is None else t.data_ptr() for t in (dx, dWq, dWk, dWv, dw0, dw1)))
     nws = LIB.cnna_core_backward_workspace(ctypes.byref(d))
     ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=x.device)
@@ -340,19 +354,21 @@ class ConvNNCore(torch.autograd.Function):
     backward fails with RuntimeError for sampled euclidean; the kernels here
     can differentiate that case, and do when this flag is off.
 
-    ``wmul``: optional (B*H, N, K) fp32 multipliers applied to the neighbour
-    weights before the aggregation (dropout on attention probabilities:
-    0 or 1/(1-p)); depthwise conv only.
+    ``dmask``: optional dense keep-mask (B, H, N, Nq) of an attention dropout
+    drawn over the whole score matrix (MultiHeadKvtAttention's ``attn_drop``,
+    layers.py:680); the kept probabilities are multiplied by
+    ``dmask[..., idx] * dscale`` (0 or 1/(1-p)); depthwise conv only.
     """
 
     @staticmethod
-    def forward(ctx, x, Wq, Wk, Wv, w0, w1, cand, d, reference_errors=False, wmul=None):
+    def forward(ctx, x, Wq, Wk, Wv, w0, w1, cand, d, reference_errors=False, dmask=None, dscale=1.0):
         q, k, v, qn, kn = project_qkv(d, x, cand, Wq, Wk, Wv)
-        idx, vals, w = select(d, k, q, kn, qn, cand)
+        idx, vals, w, cols = select_cols(d, k, q, kn, qn, cand)
+        wmul = entry_multipliers(d, idx, dmask, dscale)
         z = aggregate(d, v, idx, w if wmul is None else w * wmul, w0, w1)
         ctx.d = d
         ctx.reference_errors = reference_errors
-        ctx.save_for_backward(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul)
+        ctx.save_for_backward(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul, cols)
         return z
 
     @staticmethod
@@ -363,12 +379,22 @@ class ConvNNCore(torch.autograd.Function):
                 "one of the variables needed for gradient computation has been modified by an "
                 "inplace operation: the sampled euclidean similarity is masked in place after "
                 "sqrt (layers.py:291-292, 304-305)")
-        x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul = ctx.saved_tensors
+        x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul, cols = ctx.saved_tensors
         dx, dWq, dWk, dWv, dw0, dw1 = core_backward(ctx.d, x, cand, Wq, Wk, Wv, w0, w1,
-                                                    (q, k, v, qn, kn, idx, vals, w, wmul), dz)
+                                                    (q, k, v, qn, kn, idx, vals, w, wmul, cols), dz)
         dw0 = dw0.to(w0.dtype)
         dw1 = None if dw1 is None else dw1.to(w1.dtype)
-        return dx, dWq, dWk, dWv, dw0, dw1, None, None, None, None
+        return dx, dWq, dWk, dWv, dw0, dw1, None, None, None, None, None
+
+
+def entry_multipliers(d: Desc, idx, dmask, dscale):
+    """Per-entry multipliers (B*H, N, K) fp32 from a dense keep-mask
+    (B, H, N, Nq) at the selected columns, times the dropout scale; None
+    without a mask."""
+    if dmask is None:
+        return None
+    dm = dmask.reshape(d.B * d.H, d.N, d.Nq)
+    return dm.gather(2, idx.long()).to(torch.float32) * dscale
 
 
 class OutputProj(torch.autograd.Function):
@@ -433,21 +459,26 @@ _EMPTY = lambda like: torch.empty((0,), dtype=torch.float32, device=like.device)
 
 @torch.library.custom_op("cnna::core", mutates_args=())
 def core_op(x: torch.Tensor, Wq: torch.Tensor, Wk: torch.Tensor, Wv: torch.Tensor, w0: torch.Tensor,
-            w1: Optional[torch.Tensor], cand: Optional[torch.Tensor], wmul: Optional[torch.Tensor],
-            desc: List[int], scale: float, reference_errors: bool
+            w1: Optional[torch.Tensor], cand: Optional[torch.Tensor], dmask: Optional[torch.Tensor],
+            desc: List[int], scale: float, reference_errors: bool, dscale: float
             ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
-                       torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """x -> (z, q, k, v, qn, kn, idx, vals, w): projections, selection,
-    aggregation, head merge (layers.py:261-317); qn / kn empty when unused."""
+                       torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """x -> (z, q, k, v, qn, kn, idx, vals, w, wmul, cols): projections,
+    selection, aggregation, head merge (layers.py:261-317); qn / kn empty when
+    unused; wmul the per-entry dropout multipliers of ``dmask`` (empty
+    without); cols the sampled paths' candidate columns (empty for 'all')."""
     d = _desc_of(desc, scale)
     q, k, v, qn, kn = project_qkv(d, x, cand, Wq, Wk, Wv)
-    idx, vals, w = select(d, k, q, kn, qn, cand)
+    idx, vals, w, cols = select_cols(d, k, q, kn, qn, cand)
+    wmul = entry_multipliers(d, idx, dmask, dscale)
     z = aggregate(d, v, idx, w if wmul is None else w * wmul, w0, w1)
-    return (z, q, k, v, _EMPTY(x) if qn is None else qn, _EMPTY(x) if kn is None else kn, idx, vals, w)
+    i32 = lambda: torch.empty((0,), dtype=torch.int32, device=x.device)
+    return (z, q, k, v, _EMPTY(x) if qn is None else qn, _EMPTY(x) if kn is None else kn, idx, vals, w,
+            _EMPTY(x) if wmul is None else wmul, i32() if cols is None else cols)
 
 
 @core_op.register_fake
-def _core_fake(x, Wq, Wk, Wv, w0, w1, cand, wmul, desc, scale, reference_errors):
+def _core_fake(x, Wq, Wk, Wv, w0, w1, cand, dmask, desc, scale, reference_errors, dscale):
     B, N, C, H, Nq, K = desc[:6]
     BH, dkp = B * H, _dkp(desc)
     f32 = dict(dtype=torch.float32, device=x.device)
@@ -456,7 +487,8 @@ def _core_fake(x, Wq, Wk, Wv, w0, w1, cand, wmul, desc, scale, reference_errors)
             x.new_empty((BH, N, dkp)), torch.empty((BH * Nq if norms else 0,), **f32),
             torch.empty((BH * N if norms else 0,), **f32),
             torch.empty((BH, N, K), dtype=torch.int32, device=x.device), torch.empty((BH, N, K), **f32),
-            torch.empty((BH, N, K), **f32))
+            torch.empty((BH, N, K), **f32), torch.empty((BH, N, K) if dmask is not None else (0,), **f32),
+            torch.empty((BH, N, K) if desc[11] else (0,), dtype=torch.int32, device=x.device))
 
 
 @torch.library.custom_op("cnna::core_backward", mutates_args=())
@@ -464,7 +496,7 @@ def core_backward_op(x: torch.Tensor, Wq: torch.Tensor, Wk: torch.Tensor, Wv: to
                      w0: torch.Tensor, w1: Optional[torch.Tensor], cand: Optional[torch.Tensor],
                      q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qn: torch.Tensor, kn: torch.Tensor,
                      idx: torch.Tensor, vals: torch.Tensor, w: torch.Tensor, wmul: Optional[torch.Tensor],
-                     dz: torch.Tensor, desc: List[int], scale: float
+                     cols: Optional[torch.Tensor], dz: torch.Tensor, desc: List[int], scale: float
                      ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
                                 torch.Tensor]:
     """Gradients (dx, dWq, dWk, dWv, dw0, dw1) of ``cnna::core``; dw1 empty without w1."""
@@ -472,22 +504,25 @@ def core_backward_op(x: torch.Tensor, Wq: torch.Tensor, Wk: torch.Tensor, Wv: to
     nq = None if qn.numel() == 0 else qn
     nk = None if kn.numel() == 0 else kn
     dx, dWq, dWk, dWv, dw0, dw1 = core_backward(d, x, cand, Wq, Wk, Wv, w0, w1,
-                                                (q, k, v, nq, nk, idx, vals, w, wmul), dz)
+                                                (q, k, v, nq, nk, idx, vals, w, wmul, cols), dz)
     return dx, dWq, dWk, dWv, dw0.to(w0.dtype), (x.new_empty((0,)) if dw1 is None else dw1.to(w1.dtype))
 
 
 @core_backward_op.register_fake
-def _core_backward_fake(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul, dz, desc, scale):
+def _core_backward_fake(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul, cols, dz, desc,
+                        scale):
     return (x.new_empty(x.shape), x.new_empty(Wq.shape), x.new_empty(Wk.shape), x.new_empty(Wv.shape),
             w0.new_empty(w0.shape), (x.new_empty((0,)) if w1 is None else w1.new_empty(w1.shape)))
 
 
 def _core_setup(ctx, inputs, output):
-    x, Wq, Wk, Wv, w0, w1, cand, wmul, desc, scale, reference_errors = inputs
-    z, q, k, v, qn, kn, idx, vals, w = output
+    x, Wq, Wk, Wv, w0, w1, cand, dmask, desc, scale, reference_errors, dscale = inputs
+    z, q, k, v, qn, kn, idx, vals, w, wmul, cols = output
+    wmul = None if dmask is None else wmul
+    cols = cols if desc[11] else None
     ctx.desc, ctx.scale, ctx.reference_errors = desc, scale, reference_errors
     ctx.has_w1 = w1 is not None
-    ctx.save_for_backward(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul)
+    ctx.save_for_backward(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul, cols)
 
 
 def _core_bwd(ctx, dz, *unused):
@@ -497,10 +532,10 @@ def _core_bwd(ctx, dz, *unused):
             "one of the variables needed for gradient computation has been modified by an "
             "inplace operation: the sampled euclidean similarity is masked in place after "
             "sqrt (layers.py:291-292, 304-305)")
-    x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul = ctx.saved_tensors
+    x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul, cols = ctx.saved_tensors
     dx, dWq, dWk, dWv, dw0, dw1 = core_backward_op(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx,
-                                                   vals, w, wmul, dz.contiguous(), dl, ctx.scale)
-    return dx, dWq, dWk, dWv, dw0, (dw1 if ctx.has_w1 else None), None, None, None, None, None
+                                                   vals, w, wmul, cols, dz.contiguous(), dl, ctx.scale)
+    return dx, dWq, dWk, dWv, dw0, (dw1 if ctx.has_w1 else None), None, None, None, None, None, None
 
 
 torch.library.register_autograd("cnna::core", _core_bwd, setup_context=_core_setup)
@@ -565,12 +600,13 @@ def _register_flops():
     from torch.utils.flop_counter import register_flop_formula
 
     @register_flop_formula(torch.ops.cnna.core)
-    def _f_core(x, Wq, Wk, Wv, w0, w1, cand, wmul, desc, scale, reference_errors, *a, out_shape=None, **kw):
+    def _f_core(x, Wq, Wk, Wv, w0, w1, cand, dmask, desc, scale, reference_errors, dscale, *a,
+                out_shape=None, **kw):
         return core_flops(desc)
 
     @register_flop_formula(torch.ops.cnna.core_backward)
     def _f_core_bwd(*args, out_shape=None, **kw):
-        return 2 * core_flops(args[17])
+        return 2 * core_flops(args[18])
 
     @register_flop_formula(torch.ops.cnna.output_proj)
     def _f_oproj(z, Wo, desc, scale, *a, out_shape=None, **kw):

@@ -349,7 +349,9 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdArgs a) {
     else if (euc) coef = (ds == 0.0f) ? 0.0f : ds / my_val;   // d sqrt(d2) = 1/(2s) * d d2
     if (valid) a.coef[ebase + lane] = coef;
     int my_col = my_j;
-    if (a.sampled) my_col = (valid && coef != 0.0f) ? min(max(a.inv[my_j], 0), a.Nq - 1) : 0;
+    // sampled: the candidate column the forward selected (duplicate columns of
+    // one token carry different q rows with coordinate encoding)
+    if (a.sampled) my_col = (valid && coef != 0.0f) ? min(max(a.cols[ebase + lane], 0), a.Nq - 1) : 0;
 
     // dk_i = sum_r coef[r] * q[col(r)]  (+ metric terms)
     float dk[CPL];
@@ -501,7 +503,7 @@ CNNA_DEV int entry_key(const CsrArgs& c, int64_t ge, int i, int r) {
   const int j = c.idx[ge];
   if (c.mode == CSR_TOKEN) return j;
   if (r == 0 || j == i) return -1;             // self slot / masked column
-  const int col = c.inv[j];
+  const int col = c.cols[ge];
   return col < c.nkeys ? col : -1;
 }
 
@@ -651,14 +653,6 @@ __global__ __launch_bounds__(256) void csr_sort_kernel(CsrArgs c) {
 __global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (e < n) p[e] = v;
-}
-
-__global__ __launch_bounds__(256) void inv_map_kernel(const int32_t* cand, int Nq, int N,
-                                                      int32_t* inv) {
-  const int j = blockIdx.x * 256 + threadIdx.x;
-  if (j >= Nq) return;
-  const int t = cand[j];
-  if (t >= 0 && t < N) atomicMin(&inv[t], j);
 }
 
 // ------------------------------------------------------------------ pull
@@ -1007,13 +1001,6 @@ int launch_w0_reduce(int dtype, const float* part, int nblk, int n, void* out, h
 int launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t s) {
   if (n <= 0) return 0;
   hipLaunchKernelGGL(fill_i32_kernel, grid_for(n), dim3(256), 0, s, p, n, v);
-  return (int)hipGetLastError();
-}
-
-int launch_inv_map(const int32_t* cand, int Nq, int N, int32_t* inv, hipStream_t s) {
-  int st = launch_fill_i32(inv, N, Nq, s);
-  if (st || Nq <= 0) return st;
-  hipLaunchKernelGGL(inv_map_kernel, grid_for(Nq), dim3(256), 0, s, cand, Nq, N, inv);
   return (int)hipGetLastError();
 }
 

@@ -27,6 +27,10 @@ const char* cnna_error_string(int code) {
     case CNNA_ERR_SEQ_LENGTH: return "cnna: seq_length must equal the number of tokens when num_heads > 1";
     case CNNA_ERR_WORKSPACE: return "cnna: workspace too small";
     case CNNA_ERR_GROUPS: return "cnna: out_channels must be divisible by groups";
+    case CNNA_ERR_UNSUPPORTED:
+      return "cnna: configuration not supported by this build (limits: K <= 32 neighbours, "
+             "head width d_k (+1 with coordinate encoding) <= 256 for bfloat16 and <= 128 for "
+             "float32, at most 65536 candidates)";
     default: break;
   }
   if (code > 0) return hipGetErrorString((hipError_t)code);
@@ -43,13 +47,15 @@ int cnna_check_desc(const cnna_desc* d) {
   if (d->K < 1) return CNNA_ERR_K_RANGE;
   if (d->Nq < 0 || (!d->sampled && d->Nq != d->N)) return CNNA_ERR_SHAPE;
   if (ksel_of(d) > d->Nq) return CNNA_ERR_K_RANGE;
-  if (ksel_of(d) > 32 || d->K > 32) return CNNA_ERR_K_RANGE;
   if (d->merge != CNNA_MERGE_REFERENCE && d->merge != CNNA_MERGE_CONCAT) return CNNA_ERR_OPTION;
   if (d->scale != 0.0f && (d->metric != CNNA_MATMUL || !isfinite(d->scale))) return CNNA_ERR_OPTION;
   if (d->merge == CNNA_MERGE_REFERENCE && d->H > 1 && d->seq_length != d->N) return CNNA_ERR_SEQ_LENGTH;
+  // the reference accepts these; the kernels' register lists and tiles do not
+  if (ksel_of(d) > 32 || d->K > 32) return CNNA_ERR_UNSUPPORTED;
   const int dkp = dkp_of(d);
-  if (d->dtype == CNNA_BF16 && dkp > 256) return CNNA_ERR_SHAPE;
-  if (d->dtype == CNNA_F32 && dkp > 128) return CNNA_ERR_SHAPE;
+  if (d->dtype == CNNA_BF16 && dkp > 256) return CNNA_ERR_UNSUPPORTED;
+  if (d->dtype == CNNA_F32 && dkp > 128) return CNNA_ERR_UNSUPPORTED;
+  if (d->Nq > 65536) return CNNA_ERR_UNSUPPORTED;
   return CNNA_OK;
 }
 
@@ -126,7 +132,8 @@ int cnna_project_qkv(const cnna_desc* d, const void* x, int64_t ldx, const int32
 }
 
 int cnna_select(const cnna_desc* d, const void* k, const void* q, const float* kn, const float* qn,
-                const int32_t* cand, int32_t* idx, float* vals, float* w, void* stream) {
+                const int32_t* cand, int32_t* idx, float* vals, float* w, int32_t* cols,
+                void* stream) {
   int st = cnna_check_desc(d);
   if (st) return st;
   if (!k || !q || !idx || !vals) return CNNA_ERR_NULL;
@@ -136,12 +143,18 @@ int cnna_select(const cnna_desc* d, const void* k, const void* q, const float* k
   SelArgs a;
   memset(&a, 0, sizeof(a));
   a.k = k; a.q = q; a.kn = kn; a.qn = qn; a.cand = d->sampled ? cand : nullptr;
-  a.idx = idx; a.vals = vals; a.w = w; a.softmax = d->softmax;
+  a.idx = idx; a.vals = vals; a.w = w; a.cols = d->sampled ? cols : nullptr; a.softmax = d->softmax;
   a.BH = d->B * d->H; a.N = d->N; a.Nq = d->Nq; a.dkp = dkp_of(d);
   a.K = d->K; a.Ksel = ksel_of(d);
   a.rb_per_bh = (d->N + 127) / 128;
-  // matmul: S = k.q / d_k**0.5 (layers.py:324); cosine inputs are normalised
+  // matmul: S = k.q / d_k**0.5 (layers.py:324); cosine inputs are normalised.
+  // Raw keys rank the accumulator itself: a negative scale (KVT qk_scale)
+  // ranks -k.q with the magnitude as the value scale.
   a.kscale = (d->metric == CNNA_MATMUL) ? matmul_scale(d) : 1.0f;
+  if (d->metric == CNNA_MATMUL && !d->sampled && a.kscale < 0.0f) {
+    a.kscale = -a.kscale;
+    a.kneg = 1;
+  }
   if (d->metric == CNNA_EUCLIDEAN) {
     a.mask_val = 1.1f;                         // INF (layers.py:234)
     a.mask_key = -(a.mask_val * a.mask_val);
@@ -342,7 +355,8 @@ int cnna_forward(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* 
   if ((st = cnna_project_qkv(d, x, ldx, cand, Wq, Wk, Wv, q, k, v, euc ? qn : nullptr,
                              euc ? kn : nullptr, stream)))
     return st;
-  if ((st = cnna_select(d, k, q, euc ? kn : nullptr, euc ? qn : nullptr, cand, idx, vals, w, stream)))
+  if ((st = cnna_select(d, k, q, euc ? kn : nullptr, euc ? qn : nullptr, cand, idx, vals, w, nullptr,
+                        stream)))
     return st;
   if ((st = cnna_aggregate(d, v, idx, w, conv_w0, conv_w1, z, aws, agg_ws, stream))) return st;
   return cnna_output_proj(d, z, Wo, out, ldo, stream);

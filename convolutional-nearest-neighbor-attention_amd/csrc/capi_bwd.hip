@@ -17,7 +17,7 @@ namespace {
 struct CorePlan {
   void *dy, *t1, *dt1, *w0p, *dP, *dqkv, *dqs, *xs, *dxs, *wt;
   float *coef, *w0part, *part;
-  int32_t *cnt, *off, *tmp, *list, *cnt2, *off2, *tmp2, *list2, *inv;
+  int32_t *cnt, *off, *tmp, *list, *cnt2, *off2, *tmp2, *list2;
   size_t bytes;
 };
 
@@ -57,7 +57,6 @@ CorePlan plan_core(const cnna_desc* d, void* ws) {
     p.dqs = c.take(B * Nq * C * es);
     p.xs = c.take(B * Nq * C * es);
     p.dxs = c.take(B * Nq * C * es);
-    p.inv = static_cast<int32_t*>(c.take(N * 4));
     p.cnt2 = static_cast<int32_t*>(c.take(BH * (Nq > 0 ? Nq : 1) * 4));
     p.off2 = static_cast<int32_t*>(c.take(BH * (Nq + 1) * 4));
     p.tmp2 = static_cast<int32_t*>(c.take(ent * 4));
@@ -163,7 +162,7 @@ int cnna_core_backward(const cnna_desc* d, const void* x, int64_t ldx, const int
   if (d->metric != CNNA_MATMUL && (!sv->qn || !sv->kn)) return CNNA_ERR_NULL;
   if (!gr->dx || !gr->dWq || !gr->dWk || !gr->dWv || !gr->dconv_w0) return CNNA_ERR_NULL;
   if (d->conv == CNNA_CONV_DWSEP && (!conv_w1 || !gr->dconv_w1)) return CNNA_ERR_NULL;
-  if (d->sampled && !cand) return CNNA_ERR_NULL;
+  if (d->sampled && (!cand || !sv->cols)) return CNNA_ERR_NULL;
   if (sv->wmul && d->conv != CNNA_CONV_DEPTHWISE) return CNNA_ERR_OPTION;
   if (ldx < d->C) return CNNA_ERR_SHAPE;
   if (ws_bytes < cnna_core_backward_workspace(d)) return CNNA_ERR_WORKSPACE;
@@ -225,13 +224,12 @@ int cnna_core_backward(const cnna_desc* d, const void* x, int64_t ldx, const int
   }
 
   // 3. per token: weight / softmax / similarity backward, dK, depthwise-weight partials
-  if (d->sampled && (st = launch_inv_map(cand, Nq, N, p.inv, s))) return st;
   const int ld3 = (d->sampled ? 2 : 3) * C;
   const int offK = d->sampled ? 0 : C, offV = offK + C;
   TokBwdArgs t;
   memset(&t, 0, sizeof(t));
   t.g = g_dw; t.dP = p.dP; t.v = sv->v; t.k = sv->k; t.q = sv->q; t.kn = sv->kn;
-  t.idx = sv->idx; t.vals = sv->vals; t.w = sv->w; t.inv = p.inv; t.w0 = conv_w0;
+  t.idx = sv->idx; t.vals = sv->vals; t.w = sv->w; t.cols = sv->cols; t.w0 = conv_w0;
   t.coef = p.coef; t.w0part = p.w0part;
   t.dst = p.dqkv; t.ldd = ld3; t.offd = offK;
   t.BH = BH; t.N = N; t.Nq = Nq; t.K = K; t.din = din; t.dk = dk; t.dkp = dkp; t.H = H;
@@ -247,7 +245,7 @@ int cnna_core_backward(const cnna_desc* d, const void* x, int64_t ldx, const int
   // 4. reverse adjacency by value row; dV (and dQ for 'all') pulled in entry order
   CsrArgs c;
   memset(&c, 0, sizeof(c));
-  c.idx = sv->idx; c.inv = p.inv; c.mode = CSR_TOKEN;
+  c.idx = sv->idx; c.cols = sv->cols; c.mode = CSR_TOKEN;
   c.BH = BH; c.N = N; c.K = K; c.nkeys = N;
   c.cnt = p.cnt; c.off = p.off; c.tmp = p.tmp; c.list = p.list;
   if ((st = launch_csr(c, s))) return st;

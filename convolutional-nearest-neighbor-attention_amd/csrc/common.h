@@ -60,6 +60,12 @@ template <> struct Mfma<uint16_t> {
     return __builtin_bit_cast(frag, u);
   }
   static CNNA_DEV frag zero() { return __builtin_bit_cast(frag, make_uint4(0, 0, 0, 0)); }
+  // exact negation: flip the eight sign bits
+  static CNNA_DEV frag neg(frag a) {
+    u32x4_t u = __builtin_bit_cast(u32x4_t, a);
+    u ^= 0x80008000u;
+    return __builtin_bit_cast(frag, u);
+  }
   static CNNA_DEV f32x16_t mma(frag a, frag b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
@@ -71,6 +77,7 @@ template <> struct Mfma<float> {
   typedef float frag;
   static CNNA_DEV frag load(const float* p) { return *p; }
   static CNNA_DEV frag zero() { return 0.0f; }
+  static CNNA_DEV frag neg(frag a) { return -a; }
   static CNNA_DEV f32x16_t mma(frag a, frag b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
   }

@@ -85,9 +85,11 @@ struct SelArgs {
   int32_t* idx;      // (BH, N, K)
   float* vals;       // (BH, N, K) selected similarity values
   float* w;          // (BH, N, K) neighbour weights, or NULL
+  int32_t* cols;     // sampled: (BH, N, K) candidate column of each entry (slot 0: Nq), or NULL
   int softmax;       // softmax_topk_val
   int BH, N, Nq, dkp, K, Ksel, rb_per_bh;
-  float kscale;      // key = acc * kscale for dot metrics
+  float kscale;      // key = acc * kscale for dot metrics (raw keys: value = key * kscale, kscale > 0)
+  int kneg;          // raw keys of a negative matmul scale: rank -k.q (the key rows are negated)
   float mask_key;    // key of the self-masked candidate (sampled)
   float mask_val;    // value reported for it
 };
@@ -193,7 +195,7 @@ struct TokBwdArgs {
   const float* vals;    // (BH, N, K)
   const float* w;       // (BH, N, K)
   const float* wmul;    // (BH, N, K) multipliers applied to w before the aggregation, or NULL
-  const int32_t* inv;   // sampled: token -> candidate column (or >= Nq)
+  const int32_t* cols;  // sampled: (BH, N, K) candidate column of each entry
   const void* w0;       // depthwise weight (din, 1, K)
   float* coef;          // out: (BH, N, K) similarity-gradient coefficient
   float* w0part;        // out: (gridDim, din, K) depthwise-weight partials
@@ -214,12 +216,12 @@ inline int tok_bwd_blocks(int BH, int N) {
 int launch_w0_reduce(int dtype, const float* part, int nblk, int n, void* out, hipStream_t s);
 
 // Deterministic reverse adjacency: entries e = i*K + r of each (b, h) bucketed
-// by key (CSR_TOKEN: idx[e]; CSR_COLUMN: inv[idx[e]] for sampled r >= 1 that
-// are not the masked self column), sorted by e inside each bucket.
+// by key (CSR_TOKEN: idx[e]; CSR_COLUMN: cols[e] for sampled r >= 1 that are
+// not the masked self column), sorted by e inside each bucket.
 enum { CSR_TOKEN = 0, CSR_COLUMN = 1 };
 struct CsrArgs {
   const int32_t* idx;
-  const int32_t* inv;
+  const int32_t* cols;
   int mode;
   int BH, N, K, nkeys;
   int32_t* cnt;    // (BH, nkeys)
@@ -228,8 +230,6 @@ struct CsrArgs {
   int32_t* list;   // (BH, N*K)
 };
 int launch_csr(const CsrArgs& c, hipStream_t s);
-// inv[t] = smallest column j with cand[j] == t, or Nq
-int launch_inv_map(const int32_t* cand, int Nq, int N, int32_t* inv, hipStream_t s);
 
 // Pull reductions over a CSR: dV (sum of w * dP over the entries that read a
 // value row) and dQ (sum of coef * k over the entries that selected a column).

@@ -15,7 +15,8 @@
 //
 // Ranking key (larger is better):
 //   matmul / cosine, sampling 'all': the raw accumulator k.q (the positive
-//     scale 1/sqrt(d_k) is applied to the selected values only);
+//     scale 1/sqrt(d_k) is applied to the selected values only; a negative
+//     scale negates the key rows once, so the key is -k.q);
 //   sampled paths: acc * kscale, with the self-masked candidate set to the
 //     reference's constant;
 //   euclidean: -d^2, d^2 = (|k|^2 + |q|^2) - 2 acc; a negative d^2 (NaN
@@ -184,6 +185,11 @@ void select_kernel(SelArgs a) {
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
     kf[c] = (EXACT || c < nch) ? M_::load(Kb + c * M_::KC + half * M_::KL) : M_::zero();
+  // a negative matmul scale ranks the smallest k.q first: rank on -k.q
+  if (RAW && a.kneg) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) kf[c] = M_::neg(kf[c]);
+  }
   // wait for the key rows here, so the tile loop carries no vector-memory waits
   // ahead of its MFMAs (s_waitcnt vmcnt(0))
   __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -458,10 +464,12 @@ void select_kernel(SelArgs a) {
   constexpr int KO = KMAX + OFF;
   float vv[KO], wv[KO];
   int tk[KO];
+  int cl[KO];   // sampled: candidate column of each entry (slot 0, the token itself: Nq)
   if (half == 0 && tvalid) {
     if (SMP) {
       tk[0] = ti;
       vv[0] = 1.0f;
+      cl[0] = a.Nq;
     }
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) {
@@ -475,6 +483,7 @@ void select_kernel(SelArgs a) {
       if (SMP && EUC && tok == ti) val = a.mask_val;
       vv[OFF + r] = val;
       tk[OFF + r] = tok;
+      cl[OFF + r] = j;
     }
     // neighbour weights (layers.py:352-355, 382-385, 394-397, 426-429)
     if (a.softmax) {
@@ -514,6 +523,7 @@ void select_kernel(SelArgs a) {
   emit([&](int r) { return (uint32_t)tk[r]; }, reinterpret_cast<uint32_t*>(a.idx));
   emit([&](int r) { return __float_as_uint(vv[r]); }, reinterpret_cast<uint32_t*>(a.vals));
   if (a.w != nullptr) emit([&](int r) { return __float_as_uint(wv[r]); }, reinterpret_cast<uint32_t*>(a.w));
+  if (SMP && a.cols != nullptr) emit([&](int r) { return (uint32_t)cl[r]; }, reinterpret_cast<uint32_t*>(a.cols));
 }
 
 template <typename T, int NCH, bool EXACT, int KMAX>

@@ -135,15 +135,34 @@ class MultiHeadConvNNAttention(nn.Module):
                                 self.magnitude_type, self.convolution_type, self.softmax_topk_val,
                                 cand is not None, self.coordinate_encoding)
             z = torch.ops.cnna.core(x, Wq, Wk, Wv, _amp_cast(w0, x.dtype), _amp_cast(w1, x.dtype), cand,
-                                    None, d, 0.0, True)[0]
-            return self.dropout(z), d
+                                    None, d, 0.0, True, 1.0)[0]
+            return self._conv_output_dropout(z), d
         d = ops.make_desc(B, N, C, self.num_heads, Nq, self.K, self.seq_length, x.dtype,
                           self.magnitude_type, self.convolution_type, self.softmax_topk_val,
                           cand is not None, self.coordinate_encoding)
         z = ops.ConvNNCore.apply(x, Wq, Wk, Wv, w0, w1, cand, d, True)
-        # dropout on the conv output (layers.py:316); elementwise, so applying it
-        # after the head merge is the same operation on permuted elements
-        return self.dropout(z), d
+        return self._conv_output_dropout(z), d
+
+    def _conv_output_dropout(self, z):
+        """``self.dropout`` on the conv output y (B*H, d_k, N), where the reference
+        applies it (layers.py:316), given the head-merged z (B, N, C).
+
+        z is a permutation of y's elements; y is rebuilt contiguous in the
+        reference's layout, dropped out there (so the mask, the random numbers
+        consumed and the rounding are those of the reference's call) and merged
+        again.  Eval mode and p = 0 draw nothing and return z."""
+        if not self.training or self.dropout.p == 0:
+            return z
+        B, N, C = z.shape
+        H, dk = self.num_heads, C // self.num_heads
+        if H == 1:
+            # layers.py:248-249, 255-256: the merge is a transpose
+            y = z.transpose(1, 2).contiguous()
+            return self.dropout(y).transpose(1, 2).contiguous()
+        # z[b, t, h*d_k + a] = y_tok[b*H + h].flat[a*N + t], y_tok = y.transpose(1, 2)
+        y = z.view(B, N, H, dk).permute(0, 2, 3, 1).reshape(B * H, N, dk).transpose(1, 2).contiguous()
+        y = self.dropout(y)
+        return y.transpose(1, 2).reshape(B, H, dk, N).permute(0, 3, 1, 2).reshape(B, N, C).contiguous()
 
 
 AMP_DTYPE = torch.bfloat16
@@ -369,6 +388,13 @@ class MultiHeadBranchingAttention(_Branching):
         return self._both(x, self.attention)
 
 
+def dropout_keep_scale(p: float) -> float:
+    """The factor nn.Dropout applies to kept elements on the GPU: 1/(1-p)
+    evaluated as 1.0 / float32(1 - p) in double, then rounded to float32."""
+    import numpy as np
+    return float(np.float32(1.0 / float(np.float32(1.0 - p))))
+
+
 class MultiHeadKvtAttention(nn.Module):
     """Top-k sparse softmax attention (layers.py:654-686) on the streaming
     top-k kernel instead of a dense (B, H, N, N) score matrix and scatter mask.
@@ -379,10 +405,11 @@ class MultiHeadKvtAttention(nn.Module):
     path with the roles of the projections assigned as
     ``W_k := qkv.weight[:C]`` (rows that choose) and ``W_q := qkv.weight[C:2C]``
     (candidates), unit depthwise weights, softmax weights and the concatenated
-    head layout; forward and backward both run natively.  ``attn_drop``
-    applies to the kept probabilities (the dropped entries of the reference's
-    dense row are zero already).  Native limits: ``topk`` <= 32 and no
-    ``qkv_bias`` (NotImplementedError otherwise).
+    head layout; forward and backward both run natively.  ``attn_drop`` draws
+    the reference's dense (B, H, N, N) mask and applies it at the kept
+    probabilities (the dropped entries of the reference's dense row are zero
+    already).  Native limits: ``topk`` <= 32 and no ``qkv_bias``
+    (NotImplementedError otherwise).
     """
 
     def __init__(self, dim, num_heads=8, qkv_bias=False, qk_scale=None, attn_drop=0., proj_drop=0.,
@@ -396,6 +423,19 @@ class MultiHeadKvtAttention(nn.Module):
         self.proj = nn.Linear(dim, dim, bias=False)
         self.proj_drop = nn.Dropout(proj_drop)
         self.topk = topk
+
+    def _dense_dropout_mask(self, B, H, N, x):
+        """``attn_drop`` of the reference (layers.py:680) draws its mask over the
+        dense (B, H, N, N) probability matrix; the same draw (random numbers,
+        element order, dtype) on a tensor of ones gives the mask, whose entries
+        at the kept positions become the per-entry multipliers.  Returns
+        (mask or None, scale)."""
+        p = self.attn_drop.p
+        if not self.training or p == 0:
+            return None, 1.0
+        with torch.no_grad():
+            kept = self.attn_drop(torch.ones((B, H, N, N), dtype=x.dtype, device=x.device)) != 0
+        return kept, (dropout_keep_scale(p) if p < 1 else 0.0)
 
     def forward(self, x):
         if not x.is_cuda:
@@ -413,16 +453,14 @@ class MultiHeadKvtAttention(nn.Module):
             raise RuntimeError(f"mat1 and mat2 must have the same dtype, but got {x.dtype} and "
                                f"{W.dtype}")
         ones = torch.ones((C // H, 1, self.topk), dtype=x.dtype, device=x.device)
-        wmul = None
-        if self.training and self.attn_drop.p > 0:
-            wmul = self.attn_drop(torch.ones((B * H, N, self.topk), dtype=torch.float32, device=x.device))
+        dmask, dscale = self._dense_dropout_mask(B, H, N, x)
         if ops.use_library_ops():
             d = ops.desc_values(B, N, C, H, N, self.topk, N, x.dtype, "matmul", "depthwise", True, False,
                                 False, merge=ops.MERGE_CONCAT)
-            z = torch.ops.cnna.core(x, W[C:2 * C], W[:C], W[2 * C:], ones, None, None, wmul, d,
-                                    float(self.scale), False)[0]
+            z = torch.ops.cnna.core(x, W[C:2 * C], W[:C], W[2 * C:], ones, None, None, dmask, d,
+                                    float(self.scale), False, dscale)[0]
             return self.proj_drop(torch.ops.cnna.output_proj(z, P, d, float(self.scale)))
         d = ops.make_desc(B, N, C, H, N, self.topk, N, x.dtype, "matmul", "depthwise", True, False, False,
                           merge=ops.MERGE_CONCAT, scale=self.scale)
-        z = ops.ConvNNCore.apply(x, W[C:2 * C], W[:C], W[2 * C:], ones, None, None, d, False, wmul)
+        z = ops.ConvNNCore.apply(x, W[C:2 * C], W[:C], W[2 * C:], ones, None, None, d, False, dmask, dscale)
         return self.proj_drop(ops.OutputProj.apply(z, P, d))

@@ -32,12 +32,14 @@ from layers import (MultiHeadAttention, MultiHeadBranchingAttention, MultiHeadBr
 
 
 def vit_tiny_args(**overrides) -> SimpleNamespace:
-    """The reference CLI defaults for ViT-Tiny (main.py:32-113)."""
+    """The reference CLI defaults for ViT-Tiny (main.py:32-113); softmax_topk_val
+    is True there whatever the flags say (main.py:48-49 sets the default of a
+    store_true flag to True)."""
     a = dict(layer="ConvNNAttention", img_size=(3, 224, 224), patch_size=16, num_layers=12,
              num_heads=3, d_hidden=192, d_mlp=768, dropout=0.1, attention_dropout=0.1,
              num_classes=10, K=9, sampling_type="all", num_samples=-1, sample_padding=0,
              magnitude_type="matmul", coordinate_encoding=False, convolution_type="depthwise",
-             softmax_topk_val=False, kernel_size=9, branch_ratio=0.5)
+             softmax_topk_val=True, kernel_size=9, branch_ratio=0.5)
     a.update(overrides)
     return SimpleNamespace(**a)
 

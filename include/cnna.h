@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define CNNA_ABI_VERSION 2
+#define CNNA_ABI_VERSION 3
 
 enum cnna_dtype { CNNA_F32 = 0, CNNA_BF16 = 1 };
 /* magnitude_type (layers.py:167-168, 323-340) */
@@ -51,7 +51,9 @@ enum cnna_status {
   CNNA_ERR_K_RANGE = -5,      /* K larger than the candidates (torch.topk RuntimeError) */
   CNNA_ERR_SEQ_LENGTH = -6,   /* seq_length != N with num_heads > 1 (layers.py:251) */
   CNNA_ERR_WORKSPACE = -7,    /* workspace too small */
-  CNNA_ERR_GROUPS = -8        /* depthwise with coordinate encoding (Conv1d ValueError) */
+  CNNA_ERR_GROUPS = -8,       /* depthwise with coordinate encoding (Conv1d ValueError) */
+  CNNA_ERR_UNSUPPORTED = -9   /* a valid reference configuration beyond this library's limits
+                                 (cnna_error_string names the limit) */
 };
 
 /* Operator configuration: the constructor arguments of layers.py:133-146
@@ -112,9 +114,14 @@ int cnna_project_qkv(const cnna_desc* d, const void* x, int64_t ldx, const int32
  * 410, with the sampled self mask layers.py:291-292, 304-305).  The N x Nq
  * similarity matrix is never written.  Ties break by lowest candidate index.
  * Also writes the neighbour weights w (softmax of the values, or the raw
- * values / 1/(value + 1e-8) without softmax) when w is not NULL. */
+ * values / 1/(value + 1e-8) without softmax) when w is not NULL, and for
+ * sampled paths the candidate column of each entry, cols (B*H, N, K) int32
+ * (slot 0, the token itself: Nq), when cols is not NULL: several columns can
+ * hold one token (spatial linspace with more samples than tokens), and with
+ * coordinate encoding their q rows differ; the backward needs the column. */
 int cnna_select(const cnna_desc* d, const void* k, const void* q, const float* kn, const float* qn,
-                const int32_t* cand, int32_t* idx, float* vals, float* w, void* stream);
+                const int32_t* cand, int32_t* idx, float* vals, float* w, int32_t* cols,
+                void* stream);
 
 /* V gather and the Conv1d(kernel=K, stride=K) over the neighbours
  * (layers.py:346-358, 378-386, 393-405, 425-436, 313), then the head merge
@@ -166,6 +173,8 @@ typedef struct cnna_saved {
    * aggregation (dropout on the attention probabilities: 0 or 1/(1-p),
    * layers.py:680), or NULL; depthwise conv only */
   const float* wmul;
+  /* sampled paths: the cols output of cnna_select (required), else NULL */
+  const int32_t* cols;
 } cnna_saved;
 
 /* Gradients written by cnna_core_backward, dtype of the descriptor.

@@ -371,13 +371,17 @@ class Intermediates:
 
 def forward(x: torch.Tensor, p: Params, cfg: Config, cand: Optional[torch.Tensor] = None,
             mode: str = "reference", generator=None, return_intermediates: bool = False,
-            cols: Optional[torch.Tensor] = None):
+            cols: Optional[torch.Tensor] = None, y_dropout=None):
     """Restatement of ``MultiHeadConvNNAttention.forward`` (layers.py:261-321).
 
     ``cand`` injects the sampled candidate indices; when None they are drawn
     with ``sample_indices`` (randperm on ``generator``).  Dropout is the
-    identity (eval mode).  ``cols`` fixes the selected candidate columns (see
-    ``select_neighbours``); the function stays differentiable in x and p.
+    identity (eval mode) unless ``y_dropout`` is given: a function applied to
+    the conv output y (B*H, d_k, N) where the reference applies
+    ``self.dropout`` (layers.py:316), e.g. ``nn.Dropout`` in training mode or
+    a multiplication by a given mask.  ``cols`` fixes the selected candidate
+    columns (see ``select_neighbours``); the function stays differentiable in
+    x and p.
     """
     if mode not in ("reference", "exact"):
         raise ValueError(mode)
@@ -426,7 +430,9 @@ def forward(x: torch.Tensor, p: Params, cfg: Config, cand: Optional[torch.Tensor
         prime = gather_prime(vv, idx, w.to(prime_dtype(vv, w)), cfg)
     y = conv(prime, p.to(dtype=prime.dtype), cfg)
 
-    # 4. head merge (+dropout identity) and W_o (layers.py:316-320)
+    # 4. dropout on y (layers.py:316), head merge and W_o (layers.py:317-320)
+    if y_dropout is not None:
+        y = y_dropout(y)
     z = head_merge(y, B, H, cfg.seq_length)
     z = z.to(dt)
     out = F.linear(z, p.W_o.to(dt))
@@ -570,13 +576,16 @@ def mha(x: torch.Tensor, Wq, Wk, Wv, Wo, H: int, mask=None) -> torch.Tensor:
 
 
 def kvt(x: torch.Tensor, Wqkv, Wproj, H: int, topk: int, scale: float, wmul=None,
-        bqkv=None) -> torch.Tensor:
+        bqkv=None, dense_mult=None) -> torch.Tensor:
     """MultiHeadKvtAttention.forward (layers.py:668-686), eval mode.
 
     attn = q k^T * scale; keep the ``topk`` largest of each row (ties: lowest
     key index, see ``stable_topk``), -inf elsewhere; softmax; @ v; heads side
     by side; proj.  ``wmul`` (B*H, N, topk): multipliers on the kept
     probabilities in rank order (attention dropout with a given mask).
+    ``dense_mult`` (B, H, N, N): ``attn_drop`` as the reference applies it
+    (layers.py:680), a multiplier on the whole probability row (the
+    probabilities outside the top-k are zero).
     """
     B, N, C = x.shape
     dk = C // H
@@ -587,6 +596,8 @@ def kvt(x: torch.Tensor, Wqkv, Wproj, H: int, topk: int, scale: float, wmul=None
     p = torch.softmax(vals, dim=-1)                                  # == masked dense softmax
     if wmul is not None:
         p = p * wmul.view(B, H, N, topk).to(p.dtype)
+    if dense_mult is not None:
+        p = p * torch.gather(dense_mult.to(p.dtype), -1, idx)
     vg = torch.gather(v.unsqueeze(2).expand(B, H, N, N, dk), 3,
                       idx.unsqueeze(-1).expand(B, H, N, topk, dk))   # (B, H, N, topk, dk)
     o = (p.unsqueeze(-1) * vg).sum(3)

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert ops.LIB.cnna_abi_version() == 2
+    assert ops.LIB.cnna_abi_version() == 3
 
 
 def desc(**kw):
@@ -63,9 +63,20 @@ def test_check_desc_ok():
     (dict(scale=float("inf")), ops.ERR_OPTION),
     (dict(seq_length=197), ops.ERR_SEQ),               # H > 1 and seq_length != N
     (dict(K=0), ops.ERR_K_RANGE),
+    # valid for the reference, beyond the kernels' limits: NotImplementedError, not a range error
+    (dict(N=64, Nq=64, seq_length=64, K=33), ops.ERR_UNSUPPORTED),
+    (dict(C=3 * 264, dtype=ops.CNNA_BF16), ops.ERR_UNSUPPORTED),   # bf16 head width > 256
+    (dict(C=3 * 136), ops.ERR_UNSUPPORTED),                        # f32 head width > 128
+    (dict(N=70000, Nq=70000, seq_length=70000), ops.ERR_UNSUPPORTED),
 ])
 def test_check_desc_errors(kw, code):
     assert status(**kw) == code
+
+
+def test_negative_matmul_scale_accepted():
+    # KVT's qk_scale may be negative (layers.py:662): the kernels rank k.q * scale
+    assert status(scale=-0.25) == 0
+    assert status(scale=-0.25, merge=1, seq_length=5) == 0
 
 
 def test_concat_merge_ignores_seq_length():
@@ -87,6 +98,8 @@ def test_error_strings_and_exception_types():
         ops.check(ops.ERR_GROUPS)
     with pytest.raises(TypeError):
         ops.check(ops.ERR_DTYPE)
+    with pytest.raises(NotImplementedError, match="K <= 32"):
+        ops.check(ops.ERR_UNSUPPORTED)
     assert b"workspace" in ops.LIB.cnna_error_string(ops.ERR_WS)
 
 

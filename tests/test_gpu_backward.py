@@ -25,16 +25,16 @@ if torch.cuda.is_available():
 NAMES = ("x", "W_q", "W_k", "W_v", "W_o", "conv0", "conv1")
 
 
-def columns(idx, cand, N):
-    """GPU token indices -> candidate columns the oracle should select."""
+def columns(idx, cand, N, cols=None):
+    """The candidate columns the GPU selected, for the oracle to use: token
+    indices for sampling 'all', the select kernel's own column output for the
+    sampled paths (slot 0, the token itself, dropped)."""
     if cand is None:
         return idx.long()
-    inv = torch.full((N,), -1, dtype=torch.long)
-    for j in reversed(range(cand.numel())):
-        inv[int(cand[j])] = j
-    cols = inv[idx[..., 1:].long()]
-    assert (cols >= 0).all()
-    return cols
+    c = cols[..., 1:].long()
+    assert ((c >= 0) & (c < cand.numel())).all()
+    assert torch.equal(cand[c], idx[..., 1:].long())     # each column holds the selected token
+    return c
 
 
 def gpu_grads(cfg, p, x, cand, dout):
@@ -51,10 +51,10 @@ def gpu_grads(cfg, p, x, cand, dout):
     # the selection the forward made (kernels are deterministic)
     with torch.no_grad():
         q, k, v, qn, kn = ops.project_qkv(d, xg.detach(), cg, Wq.detach(), Wk.detach(), Wv.detach())
-        idx, vals, w = ops.select(d, k, q, kn, qn, cg)
+        idx, vals, w, cols = ops.select_cols(d, k, q, kn, qn, cg)
     torch.cuda.synchronize()
     grads = {n: (None if t is None else t.grad.detach().cpu()) for n, t in zip(NAMES, ts)}
-    return out.detach().cpu(), grads, idx.cpu()
+    return out.detach().cpu(), grads, columns(idx.cpu(), cand, N, None if cols is None else cols.cpu())
 
 
 def oracle_grads(cfg, p, x, cand, dout, cols):
@@ -87,8 +87,8 @@ def test_backward_fp32(name, kw, B, N):
     p, x = make(cfg, B, N, torch.float32, seed=5)
     cand = cand_for(cfg, N)
     dout = torch.randn(B, N, cfg.d_hidden, generator=torch.Generator().manual_seed(7))
-    out, got, idx = gpu_grads(cfg, p, x, cand, dout)
-    out_e, exp = oracle_grads(cfg, p, x, cand, dout, columns(idx, cand, N))
+    out, got, cols = gpu_grads(cfg, p, x, cand, dout)
+    out_e, exp = oracle_grads(cfg, p, x, cand, dout, cols)
     torch.testing.assert_close(out.double(), out_e, rtol=1e-3, atol=1e-4)
     assert_grads_fp32(got, exp)
 
@@ -99,6 +99,10 @@ BWD_EXTRA = [
     ("euclid_all_raw_dw", dict(d_hidden=48, num_heads=3, K=4, magnitude_type="euclidean", softmax_topk_val=False, seq_length=40), 2, 40),
     ("cosine_random_raw_dws", dict(d_hidden=64, num_heads=2, K=6, sampling_type="random", num_samples=16, magnitude_type="cosine", softmax_topk_val=False, convolution_type="depthwise-separable", seq_length=48), 2, 48),
     ("spatial_dup_columns", dict(d_hidden=48, num_heads=3, K=5, sampling_type="spatial", num_samples=40, seq_length=24), 2, 24),
+    # duplicate columns whose q rows differ (coordinate channel over the columns),
+    # cosine normalisation over that channel: the backward must use the selected column
+    ("spatial_dup_cosine_coord", dict(d_hidden=48, num_heads=3, K=6, sampling_type="spatial", num_samples=40, magnitude_type="cosine", coordinate_encoding=True, convolution_type="standard", seq_length=24), 2, 24),
+    ("spatial_dup_matmul_coord_dws", dict(d_hidden=32, num_heads=2, K=5, sampling_type="spatial", num_samples=30, coordinate_encoding=True, convolution_type="depthwise-separable", seq_length=17), 2, 17),
     ("k32_dk128", dict(d_hidden=256, num_heads=2, K=32, seq_length=80), 2, 80),
     ("dk128_std_k16", dict(d_hidden=256, num_heads=2, K=16, convolution_type="standard", seq_length=64), 1, 64),
     # depthwise with 20-channel heads: the vector weight-gradient path (fp32, 5 vectors per row)
@@ -122,8 +126,8 @@ def test_backward_bf16(conv, N, C, K):
     B = 2
     p, x = make(cfg, B, N, torch.bfloat16, seed=11)
     dout = torch.randn(B, N, C, generator=torch.Generator().manual_seed(13)).to(torch.bfloat16)
-    out, got, idx = gpu_grads(cfg, p, x, None, dout)
-    out_e, exp = oracle_grads(cfg, p, x, None, dout, columns(idx, None, N))
+    out, got, cols = gpu_grads(cfg, p, x, None, dout)
+    out_e, exp = oracle_grads(cfg, p, x, None, dout, cols)
     assert rel_l2(out, out_e) < 2e-2
     for n in NAMES:
         if exp[n] is None:
@@ -180,3 +184,25 @@ def test_module_sampled_euclidean_backward_raises_like_reference():
     out = m(x)
     with pytest.raises(RuntimeError):
         out.sum().backward()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_output_proj_backward_with_noncontiguous_z(dtype):
+    """z reaching W_o may be a permuted view (the dropout re-layout of the
+    training path): the gradients come back row-major and correct."""
+    B, N, C = 2, 40, 96
+    d = ops.make_desc(B, N, C, 3, N, 9, N, dtype, "matmul", "depthwise", True, False, False)
+    base = torch.randn(B, C, N, device=DEV).to(dtype)
+    z = base.transpose(1, 2).requires_grad_(True)            # (B, N, C), strides (C*N, 1, N)
+    z.retain_grad()
+    assert not z.is_contiguous()
+    Wo = (torch.randn(C, C, device=DEV) / C ** 0.5).to(dtype).requires_grad_(True)
+    g = torch.randn(B, N, C, device=DEV).to(dtype)
+    out = ops.OutputProj.apply(z, Wo, d)
+    out.backward(g)
+    zz, WW, gg = (t.detach().double().cpu() for t in (z, Wo, g))
+    tol = dict(rtol=1e-4, atol=1e-4) if dtype == torch.float32 else dict(rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(out.detach().double().cpu(), zz @ WW.T, **tol)
+    torch.testing.assert_close(z.grad.double().cpu(), gg @ WW, **tol)
+    torch.testing.assert_close(Wo.grad.double().cpu(), gg.reshape(-1, C).T @ zz.reshape(-1, C),
+                               rtol=tol["rtol"], atol=tol["atol"] * 10)

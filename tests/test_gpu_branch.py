@@ -170,6 +170,7 @@ def _kvt_oracle(m, x, wmul=None):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B,N,C,H,topk,qs", [(8, 197, 192, 3, 9, None), (4, 256, 128, 1, 16, None),
                                              (3, 100, 96, 2, 1, 0.3), (2, 40, 64, 4, 32, None),
+                                             (3, 100, 96, 2, 5, -0.3),
                                              (2, 12, 48, 3, 12, None)])
 def test_kvt_forward_matches_oracle(dtype, B, N, C, H, topk, qs):
     m = _kvt(dtype, C, H, topk, qk_scale=qs)
@@ -233,13 +234,17 @@ def test_kvt_attention_dropout_forward_and_backward():
     x = torch.randn(B, N, 96, device=DEV, requires_grad=True)
     torch.manual_seed(5)
     y = m(x)
-    torch.manual_seed(5)                 # the same draw: the module's dropout on a ones tensor
-    wmul = F.dropout(torch.ones(B * 3, N, 9, device=DEV), 0.25, True)
-    assert 0 < (wmul == 0).float().mean().item() < 0.5
+    after = torch.rand(16, device=DEV)
+    # the reference's draw: attn_drop on the dense (B, H, N, N) probabilities (layers.py:680)
+    torch.manual_seed(5)
+    dense = F.dropout(torch.ones(B, 3, N, N, device=DEV), 0.25, True)
+    assert torch.equal(torch.rand(16, device=DEV), after)      # same random numbers consumed
+    assert 0 < (dense == 0).float().mean().item() < 0.5
     y.square().sum().backward()
     xc = x.detach().double().cpu().requires_grad_(True)
     Wqkv = m.qkv.weight.detach().double().cpu().requires_grad_(True)
-    yo = O.kvt(xc, Wqkv, m.proj.weight.detach().double().cpu(), 3, 9, m.scale, wmul=wmul.double().cpu())
+    yo = O.kvt(xc, Wqkv, m.proj.weight.detach().double().cpu(), 3, 9, m.scale,
+               dense_mult=dense.double().cpu())
     torch.testing.assert_close(y.detach().double().cpu(), yo.detach(), rtol=1e-3, atol=1e-3)
     yo.square().sum().backward()
     torch.testing.assert_close(x.grad.double().cpu(), xc.grad, rtol=2e-3, atol=2e-3)

@@ -51,7 +51,7 @@ def test_fake_core_outputs():
         w0 = torch.ones(32, 1, 5, dtype=torch.bfloat16)
         d = ops.desc_values(2, 100, 96, 3, 100, 5, 100, torch.bfloat16, "cosine", "depthwise", True,
                             False, False)
-        z, q, k, v, qn, kn, idx, vals, w = torch.ops.cnna.core(x, *W, w0, None, None, None, d, 0.0, True)
+        z, q, k, v, qn, kn, idx, vals, w, wm, cols = torch.ops.cnna.core(x, *W, w0, None, None, None, d, 0.0, True, 1.0)
     assert z.shape == (2, 100, 96) and z.dtype == torch.bfloat16
     assert q.shape == k.shape == v.shape == (6, 100, 32)
     assert qn.shape == kn.shape == (600,)

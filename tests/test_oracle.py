@@ -16,7 +16,10 @@ import torch.nn.functional as F
 
 from oracle import cnna_oracle as O
 
-GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
+# eval-mode fixtures (make_golden.py); the training-mode dropout fixtures
+# (make_golden_dropout.py, dropout_*.npz) are checked in test_dropout_cpu.py
+GOLDEN = sorted(p for p in glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz"))
+                if not os.path.basename(p).startswith("dropout_"))
 
 
 def load_case(path):
