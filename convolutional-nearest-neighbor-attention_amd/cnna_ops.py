@@ -25,6 +25,8 @@ MERGE_REFERENCE, MERGE_CONCAT = 0, 1
 
 ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_OPTION, ERR_K_RANGE, ERR_SEQ, ERR_WS, ERR_GROUPS, ERR_UNSUPPORTED = (
     -1, -2, -3, -4, -5, -6, -7, -8, -9)
+ERR_SCRATCH = -10
+NOALLOC_SCRATCH_BYTES = 128 << 20    # CNNA_NOALLOC_SCRATCH_BYTES
 
 
 class Desc(ctypes.Structure):
@@ -68,6 +70,7 @@ def _load():
         "cnna_output_proj": ([D, P, P, P, I64, P], I32),
         "cnna_forward_workspace": ([D], ctypes.c_size_t),
         "cnna_forward": ([D, P, I64, P, P, P, P, P, P, P, P, I64, P, ctypes.c_size_t, P], I32),
+        "cnna_forward_noalloc": ([D, P, I64, P, P, P, P, P, P, P, P, I64, P], I32),
         "cnna_output_proj_backward_workspace": ([D], ctypes.c_size_t),
         "cnna_output_proj_backward": ([D, P, P, P, I64, P, P, P, ctypes.c_size_t, P], I32),
         "cnna_core_backward_workspace": ([D], ctypes.c_size_t),
@@ -92,7 +95,7 @@ if LIB.cnna_abi_version() != ABI_VERSION:
                       "`python convolutional-nearest-neighbor-attention_amd/build.py`")
 EXPORTED = ("cnna_abi_version", "cnna_error_string", "cnna_check_desc", "cnna_head_stride",
             "cnna_project_qkv", "cnna_select", "cnna_aggregate_workspace", "cnna_aggregate",
-            "cnna_output_proj", "cnna_forward_workspace", "cnna_forward",
+            "cnna_output_proj", "cnna_forward_workspace", "cnna_forward", "cnna_forward_noalloc",
             "cnna_output_proj_backward_workspace", "cnna_output_proj_backward",
             "cnna_core_backward_workspace", "cnna_core_backward", "cnna_layernorm", "cnna_linear",
             "cnna_conv1d_branch_workspace", "cnna_conv1d_branch")
@@ -234,6 +237,18 @@ def forward_fused(d: Desc, x, cand, Wq, Wk, Wv, Wo, w0, w1=None):
     check(LIB.cnna_forward(ctypes.byref(d), _ptr(x), x.stride(1), _ptr(cand), _ptr(Wq.contiguous()),
                            _ptr(Wk.contiguous()), _ptr(Wv.contiguous()), _ptr(Wo.contiguous()),
                            _ptr(w0), _ptr(w1), _ptr(out), d.C, _ptr(ws), ws_bytes, _stream()))
+    return out
+
+
+def forward_noalloc(d: Desc, x, cand, Wq, Wk, Wv, Wo, w0, w1=None, out=None):
+    """Whole forward through ``cnna_forward_noalloc``: the library works in its
+    static device scratch (no workspace); ``out`` may be passed in so that the
+    call allocates nothing on this side either."""
+    x = x.contiguous()
+    if out is None:
+        out = torch.empty((d.B, d.N, d.C), dtype=x.dtype, device=x.device)
+    check(LIB.cnna_forward_noalloc(ctypes.byref(d), _ptr(x), x.stride(1), _ptr(cand), _ptr(Wq), _ptr(Wk),
+                                   _ptr(Wv), _ptr(Wo), _ptr(w0), _ptr(w1), _ptr(out), d.C, _stream()))
     return out
 
 

@@ -27,6 +27,9 @@ const char* cnna_error_string(int code) {
     case CNNA_ERR_SEQ_LENGTH: return "cnna: seq_length must equal the number of tokens when num_heads > 1";
     case CNNA_ERR_WORKSPACE: return "cnna: workspace too small";
     case CNNA_ERR_GROUPS: return "cnna: out_channels must be divisible by groups";
+    case CNNA_ERR_SCRATCH:
+      return "cnna: the call needs more intermediate memory than the 128 MiB static scratch of "
+             "cnna_forward_noalloc; call cnna_forward with a workspace";
     case CNNA_ERR_UNSUPPORTED:
       return "cnna: configuration not supported by this build (limits: K <= 32 neighbours, "
              "head width d_k (+1 with coordinate encoding) <= 256 for bfloat16 and <= 128 for "

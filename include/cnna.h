@@ -52,8 +52,10 @@ enum cnna_status {
   CNNA_ERR_SEQ_LENGTH = -6,   /* seq_length != N with num_heads > 1 (layers.py:251) */
   CNNA_ERR_WORKSPACE = -7,    /* workspace too small */
   CNNA_ERR_GROUPS = -8,       /* depthwise with coordinate encoding (Conv1d ValueError) */
-  CNNA_ERR_UNSUPPORTED = -9   /* a valid reference configuration beyond this library's limits
+  CNNA_ERR_UNSUPPORTED = -9,  /* a valid reference configuration beyond this library's limits
                                  (cnna_error_string names the limit) */
+  CNNA_ERR_SCRATCH = -10      /* the call needs more than the static scratch of
+                                 cnna_forward_noalloc (CNNA_NOALLOC_SCRATCH_BYTES) */
 };
 
 /* Operator configuration: the constructor arguments of layers.py:133-146
@@ -151,6 +153,24 @@ int cnna_forward(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* 
                  const void* Wq, const void* Wk, const void* Wv, const void* Wo,
                  const void* conv_w0, const void* conv_w1, void* out, int64_t ldo,
                  void* ws, size_t ws_bytes, void* stream);
+
+/* Size of the file-scope device array cnna_forward_noalloc works in. */
+#define CNNA_NOALLOC_SCRATCH_BYTES (128u << 20)
+
+/* cnna_forward without a workspace argument, for callers that cannot
+ * allocate device memory (HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference (its forward is
+ * eager PyTorch that allocates every intermediate, layers.py:261-321).
+ * The intermediates live in a static device array of
+ * CNNA_NOALLOC_SCRATCH_BYTES per GPU, held from the first call until the
+ * process ends; it allocates and frees nothing.  Returns CNNA_ERR_SCRATCH
+ * when cnna_forward_workspace(d) exceeds that size (c3, B=32 N=1024 C=384 in
+ * bf16, needs 112 MB).  Calls on one GPU share the array: calls that overlap
+ * on one GPU race; results are those of cnna_forward. */
+int cnna_forward_noalloc(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* cand,
+                         const void* Wq, const void* Wk, const void* Wv, const void* Wo,
+                         const void* conv_w0, const void* conv_w1, void* out, int64_t ldo,
+                         void* stream);
 
 /* ------------------------------------------------------------ backward
  * Autograd of the stages above (what loss.backward() computes through

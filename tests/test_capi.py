@@ -143,3 +143,17 @@ def test_module_matches_reference_parameter_names_and_init():
         assert p.W_q.shape == (12, 12)
         if conv == "depthwise":
             assert torch.all(p.conv0 == 1.0) and p.conv0.shape == (4, 1, 4)
+
+
+def test_noalloc_scratch_limit():
+    """cnna_forward_noalloc works in a static 128 MiB device array: the c3
+    layer fits, the c5 one is rejected with CNNA_ERR_SCRATCH before any device
+    call (so this runs without a GPU)."""
+    c3 = desc(B=32, N=1024, Nq=1024, C=384, H=3, K=9, seq_length=1024, dtype=ops.CNNA_BF16)
+    assert ops.LIB.cnna_forward_workspace(ctypes.byref(c3)) <= ops.NOALLOC_SCRATCH_BYTES
+    c5 = desc(B=8, N=4096, Nq=4096, C=768, H=3, K=16, seq_length=4096, dtype=ops.CNNA_BF16, conv=0)
+    assert ops.LIB.cnna_forward_workspace(ctypes.byref(c5)) > ops.NOALLOC_SCRATCH_BYTES
+    st = ops.LIB.cnna_forward_noalloc(ctypes.byref(c5), None, 768, None, None, None, None, None, None, None,
+                                      None, 768, None)
+    assert st == ops.ERR_SCRATCH
+    assert b"128 MiB" in ops.LIB.cnna_error_string(ops.ERR_SCRATCH)
