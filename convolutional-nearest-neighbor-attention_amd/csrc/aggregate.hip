@@ -46,6 +46,14 @@ template <> struct Vec<uint16_t, 8> {
     for (int i = 0; i < 4; ++i) w[i] = f2bf2(o[2 * i], o[2 * i + 1]);
     *reinterpret_cast<u32x4_t*>(p) = w;
   }
+  static CNNA_DEV Raw pack(const float (&o)[8]) {
+    Raw u;
+    u.x = f2bf2(o[0], o[1]);
+    u.y = f2bf2(o[2], o[3]);
+    u.z = f2bf2(o[4], o[5]);
+    u.w = f2bf2(o[6], o[7]);
+    return u;
+  }
 };
 template <> struct Vec<float, 4> {
   typedef float4 Raw;
@@ -57,16 +65,21 @@ template <> struct Vec<float, 4> {
   static CNNA_DEV void store(float* p, const float (&o)[4]) {
     *reinterpret_cast<float4*>(p) = make_float4(o[0], o[1], o[2], o[3]);
   }
+  static CNNA_DEV Raw pack(const float (&o)[4]) { return make_float4(o[0], o[1], o[2], o[3]); }
 };
 template <typename T> struct Vec<T, 1> {
   static CNNA_DEV void load(const T* p, float (&o)[1]) { o[0] = ldf(p); }
   static CNNA_DEV void store(T* p, const float (&o)[1]) { stf(p, o[0]); }
 };
 
-// KM > 0: K <= KM, and all K neighbour rows of two tokens are loaded before
-// any is used (one memory latency per two tokens instead of K per token)
+// KM > 0: K <= KM; the K neighbour rows of the next token group are loaded
+// while the current group is convolved
+// blocks per CU the register budget is held to: three for K <= 9 (one round
+// of blocks at the config-3 shape), two for the K <= 16 instance
+template <int KM> constexpr int agg_min_blocks() { return KM == 0 ? 1 : (KM <= 9 ? 3 : 1); }
+
 template <typename T, int VW, bool COPY, int KM>
-__global__ __launch_bounds__(256) void agg_kernel(AggArgs a) {
+__global__ __launch_bounds__(256, agg_min_blocks<KM>()) void agg_kernel(AggArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x;
   const int total = a.BH * a.nblk;
@@ -89,6 +102,8 @@ __global__ __launch_bounds__(256) void agg_kernel(AggArgs a) {
 
   if (!COPY) {
     const T* W0 = static_cast<const T*>(a.w0);
+    // (K, dout) fp32 conv weights: a lane reads its VW channels of a tap as
+    // 16-byte vectors
     for (int e = tid; e < a.K * dout; e += 256) {
       const int c = e / a.K, r = e - c * a.K;
       sW[r * dout + c] = W0 != nullptr ? ldf(W0 + e) : 1.0f;
@@ -132,42 +147,76 @@ __global__ __launch_bounds__(256) void agg_kernel(AggArgs a) {
   };
 
   if constexpr (!COPY && KM > 0) {
-    // two tokens per pass: the K neighbour rows of both are in flight at once
+    // Software-pipelined gather: the K neighbour rows of the next token group
+    // are in flight while the current group is convolved.  Per element: one
+    // unpack, one multiply by the neighbour weight, one FMA with the conv
+    // weight (fp32 LDS vectors); gather offsets in 32 bits; the staged
+    // position (row a, column t of the merge) stepped, not divided.
     typedef typename Vec<T, VW>::Raw Raw;
     const int step = 256 / LPT;
-    auto conv = [&](int tt, const Raw (&raw)[KM], float (&acc)[VW]) __attribute__((always_inline)) {
-#pragma unroll
-      for (int u = 0; u < VW; ++u) acc[u] = 0.0f;
-#pragma unroll
-      for (int r = 0; r < KM; ++r) {
-        if (r < a.K) {
-          const float wr = sw[tt * a.K + r];
-          float vv[VW];
-          Vec<T, VW>::unpack(raw[r], vv);
-#pragma unroll
-          for (int u = 0; u < VW; ++u) acc[u] += sW[r * dout + c0 + u] * (wr * vv[u]);
-        }
-      }
-    };
-    for (int tt = tid / LPT; tt < ntok; tt += 2 * step) {
-      if (c0 >= dout) continue;
-      const int tt2 = tt + step;
-      const bool two = tt2 < ntok;
-      Raw raw[KM], raw2[KM];
-#pragma unroll
-      for (int r = 0; r < KM; ++r)
-        if (r < a.K) raw[r] = Vec<T, VW>::raw(V + (int64_t)sj[tt * a.K + r] * a.dkp + c0);
-      if (two) {
+    if (c0 < dout) {
+      auto load = [&](int tt, Raw (&raw)[KM]) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < KM; ++r)
-          if (r < a.K) raw2[r] = Vec<T, VW>::raw(V + (int64_t)sj[tt2 * a.K + r] * a.dkp + c0);
-      }
-      float acc[VW];
-      conv(tt, raw, acc);
-      emit(i0 + tt, acc);
-      if (two) {
-        conv(tt2, raw2, acc);
-        emit(i0 + tt2, acc);
+          if (r < a.K) raw[r] = Vec<T, VW>::raw(V + (uint32_t)(sj[tt * a.K + r] * a.dkp + c0));
+      };
+      // merge position of (token i0 + tt, channel c0) and its step per pass
+      int tt0 = tid / LPT;
+      int f0 = (i0 + tt0) * dout + c0;
+      int za = f0 / a.N, zt = f0 - za * a.N;
+      const int dstep = step * dout;
+      const int qa = dstep / a.N, qt = dstep - qa * a.N;
+      const bool fastv = (a.N % VW) == 0;
+      auto conv_emit = [&](int tt, const Raw (&raw)[KM]) __attribute__((always_inline)) {
+        float acc[VW];
+#pragma unroll
+        for (int u = 0; u < VW; ++u) acc[u] = 0.0f;
+#pragma unroll
+        for (int r = 0; r < KM; ++r) {
+          if (r < a.K) {
+            const float wr = sw[tt * a.K + r];
+            float vv[VW];
+            Vec<T, VW>::unpack(raw[r], vv);
+            const float4* wp = reinterpret_cast<const float4*>(sW + r * dout + c0);
+#pragma unroll
+            for (int q4 = 0; q4 < VW / 4; ++q4) {
+              const float4 w4 = wp[q4];
+              acc[4 * q4 + 0] += w4.x * (wr * vv[4 * q4 + 0]);
+              acc[4 * q4 + 1] += w4.y * (wr * vv[4 * q4 + 1]);
+              acc[4 * q4 + 2] += w4.z * (wr * vv[4 * q4 + 2]);
+              acc[4 * q4 + 3] += w4.w * (wr * vv[4 * q4 + 3]);
+            }
+          }
+        }
+        if (stage_z) {
+          T* dst = stage + (za - a_lo) * NP + zt;
+          if (fastv) {
+            Vec<T, VW>::store(dst, acc);                  // one 16-byte LDS write
+          } else {
+            int aa = za, t = zt;
+#pragma unroll
+            for (int u = 0; u < VW; ++u) {
+              stf(stage + (aa - a_lo) * NP + t, acc[u]);
+              if (++t == a.N) { t = 0; ++aa; }
+            }
+          }
+          zt += qt;
+          za += qa;
+          if (zt >= a.N) { zt -= a.N; ++za; }
+        } else {
+          emit(i0 + tt, acc);
+        }
+      };
+      Raw ra[KM], rb[KM];
+      int tt = tt0;
+      if (tt < ntok) load(tt, ra);
+      // two steps per iteration so the buffers alternate without copies
+      for (; tt < ntok; tt += 2 * step) {
+        if (tt + step < ntok) load(tt + step, rb);
+        conv_emit(tt, ra);
+        if (tt + step >= ntok) break;
+        if (tt + 2 * step < ntok) load(tt + 2 * step, ra);
+        conv_emit(tt + step, rb);
       }
     }
   } else {
@@ -199,18 +248,21 @@ __global__ __launch_bounds__(256) void agg_kernel(AggArgs a) {
   const int64_t F1 = (int64_t)(i0 + ntok) * dout;
   const int na = (int)((F1 - 1) / a.N) - a_lo + 1;
   constexpr int ZV = 16 / sizeof(T);
-  if (F0 % a.N == 0 && F1 % a.N == 0 && na == ZV && (h * dout + a_lo) % ZV == 0 && a.C % ZV == 0) {
-    // the block covers ZV whole columns of Z (16 aligned bytes per row): a
-    // thread per row t gathers them from the ZV staged rows, one 16-byte store
+  if (F0 % a.N == 0 && F1 % a.N == 0 && na % ZV == 0 && (h * dout + a_lo) % ZV == 0 && a.C % ZV == 0) {
+    // the block covers na whole columns of Z, a multiple of ZV (16 aligned
+    // bytes per row and group): a thread per (row t, column group) gathers the
+    // group from ZV staged rows, one 16-byte store
     T* Zb = static_cast<T*>(a.out) + (int64_t)b * a.N * a.C + h * dout + a_lo;
-    for (int t = tid; t < a.N; t += 256) {
+    const int ng = na / ZV;
+    for (int e = tid; e < a.N * ng; e += 256) {
+      const int gq = e / a.N, t = e - gq * a.N;
       union {
         u32x4_t u;
         T e[ZV];
       } pk;
 #pragma unroll
-      for (int u = 0; u < ZV; ++u) pk.e[u] = stage[u * NP + t];
-      *reinterpret_cast<u32x4_t*>(Zb + (int64_t)t * a.C) = pk.u;
+      for (int u = 0; u < ZV; ++u) pk.e[u] = stage[(gq * ZV + u) * NP + t];
+      *reinterpret_cast<u32x4_t*>(Zb + (int64_t)t * a.C + gq * ZV) = pk.u;
     }
     return;
   }
@@ -237,11 +289,12 @@ int launch_vw(const AggArgs& a0, hipStream_t s) {
   while (lpt < (a.dout + vw - 1) / vw) lpt <<= 1;
   if (lpt > 256) return CNNA_ERR_SHAPE;
   a.lpt = lpt;
-  // tokens per block: about eight Z columns per row when merging, within LDS
+  // tokens per block: about sixteen Z columns per row when merging (two
+  // 16-byte vectors per row of the write-back), within LDS
   const bool stage_z = merge_mixes(a);
-  int ti = 64;
+  int ti = 128;
   if (stage_z) {
-    ti = (int)cnna_round_up((size_t)((8LL * a.N + a.dout - 1) / a.dout), 16);
+    ti = (int)cnna_round_up((size_t)((16LL * a.N + a.dout - 1) / a.dout), 16);
     ti = ti < 16 ? 16 : (ti > 256 ? 256 : ti);
   }
   auto lds = [&](int t) {
