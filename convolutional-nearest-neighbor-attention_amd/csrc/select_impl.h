@@ -84,6 +84,12 @@ CNNA_DEV void list_insert(uint64_t (&L)[KMAX], uint64_t x) {
 // max(a, b) for non-NaN inputs as one v_med3_f32 (fmaxf would first
 // canonicalise both operands, two more VALU ops)
 CNNA_DEV float max2(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, INFINITY); }
+// max of three non-NaN floats, one VALU op
+CNNA_DEV float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 
 template <int KMAX>
 CNNA_DEV void bound_insert(float (&L)[KMAX], float x) {
@@ -356,12 +362,12 @@ void select_kernel(SelArgs a) {
         } else if (fine) {
 #pragma unroll
           for (int g = 0; g < 4; ++g)
-            bound_insert<KMAX>(L, max2(max2(key[4 * g], key[4 * g + 1]), max2(key[4 * g + 2], key[4 * g + 3])));
+            bound_insert<KMAX>(L, max2(max3(key[4 * g], key[4 * g + 1], key[4 * g + 2]), key[4 * g + 3]));
         } else {
-          float gm = key[0];
-#pragma unroll
-          for (int v = 1; v < 16; ++v) gm = max2(gm, key[v]);
-          bound_insert<KMAX>(L, gm);
+          const float m0 = max3(key[0], key[1], key[2]), m1 = max3(key[3], key[4], key[5]);
+          const float m2 = max3(key[6], key[7], key[8]), m3 = max3(key[9], key[10], key[11]);
+          const float m4 = max3(key[12], key[13], key[14]);
+          bound_insert<KMAX>(L, max2(max3(m0, m1, m2), max3(m3, m4, key[15])));
         }
       }
     };
