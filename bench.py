@@ -111,6 +111,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-also", action="store_true",
+                    help="c3 only: skip the short c2 / c5 measurements carried on the line")
     ap.add_argument("--cpu-sample-batch", type=int, default=8)
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/traffic.json from two rocprofv3 --pmc runs of this script")
@@ -263,7 +265,7 @@ def run_vit(args):
         "model": {"flops": f_total, "tflops": round(f_total / (ms / 1e3) / 1e12, 2)},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(rec), flush=True)
+    return rec
 
 
 def kvt_dense(x, Wqkv, Wproj, H, topk, scale):
@@ -399,6 +401,16 @@ def run_callers(args):
     print(json.dumps(rec), flush=True)
 
 
+def summary(rec):
+    """The figures of a secondary workload carried on the primary JSON line."""
+    out = {k: rec[k] for k in ("metric", "value", "unit", "ms_per_step", "steps", "warmup") if k in rec}
+    out["roofline"] = {k: rec["roofline"][k] for k in ("kernel", "bound", "achieved", "unit", "frac")}
+    for k in ("stages_ms", "gather_stage", "stage_roofline"):
+        if rec.get(k) is not None:
+            out[k] = rec[k]
+    return out
+
+
 def main():
     args = parse()
     if args.summarize_pmc:
@@ -409,11 +421,29 @@ def main():
                           "n_gpus": args.gpus}))
         sys.exit(2)
     if args.config == "c2":
-        run_vit(args)
+        print(json.dumps(run_vit(args)), flush=True)
         return
     if args.config in CALLERS:
         run_callers(args)
         return
+    rec = run_layer(args)
+    if args.config == "c3" and not args.no_also:
+        # the other GPU workloads, timed in the same run with short step counts
+        # (their own bench lines: --config c2 / --config c5)
+        import copy
+        also = {}
+        a2 = copy.copy(args)
+        a2.steps, a2.warmup, a2.no_cpu, a2.config = 10, 3, True, "c2"
+        also["c2"] = summary(run_vit(a2))
+        a5 = copy.copy(args)
+        a5.steps, a5.warmup, a5.no_cpu, a5.config = 5, 2, True, "c5"
+        also["c5"] = summary(run_layer(a5))
+        rec["also"] = also
+    print(json.dumps(rec), flush=True)
+
+
+def run_layer(args):
+    """One MultiHeadConvNNAttention config (forward, or a training step for c5)."""
     import cnna_ops as ops
     from layers import MultiHeadConvNNAttention
 
@@ -488,8 +518,10 @@ def main():
     work = {
         "project": ("mfma", 2 * B * C * C * (2 * N + Nq)),
         "select": ("mfma", sim_f),
-        # read V, write y, read int32 index + fp32 value per neighbour
-        "aggregate": ("hbm", 2 * B * N * C * es + B * H * N * K * 8),
+        # depthwise: read V, write y, read int32 index + fp32 value per neighbour
+        # (HBM-bound); standard / depthwise-separable: the conv GEMM (MFMA)
+        "aggregate": (("hbm", 2 * B * N * C * es + B * H * N * K * 8) if conv == "depthwise"
+                      else ("mfma", conv_f)),
         "output_proj": ("mfma", 2 * B * N * C * C),
     }
     dom = max(st_ms, key=st_ms.get)
@@ -506,6 +538,25 @@ def main():
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                 "traffic": measured_traffic(args.config, dom)}
 
+    # every stage against its own roof (HIP-event medians above); the gather /
+    # conv stage is HBM-bound: v read, z written, int32 index + fp32 weight read
+    stage_roof = {}
+    for name, (bnd, amt) in work.items():
+        t_st = st_ms[name] / 1e3
+        if bnd == "mfma":
+            ach = amt / t_st / 1e12
+            stage_roof[name] = {"bound": "mfma", "achieved_TFLOPs": round(ach, 1), "frac": round(ach / peak_mfma, 4)}
+        else:
+            ach = amt / t_st / 1e9
+            stage_roof[name] = {"bound": "hbm", "achieved_GBs": round(ach, 1), "frac": round(ach / PEAK_HBM_GBS, 4)}
+    gather = None
+    if conv == "depthwise":
+        agg_bytes = work["aggregate"][1]
+        gather = {"kernel": "aggregate", "bound": "hbm", "bytes": agg_bytes, "ms": round(st_ms["aggregate"], 4),
+                  "achieved_GBs": round(agg_bytes / (st_ms["aggregate"] / 1e3) / 1e9, 1), "peak_GBs": PEAK_HBM_GBS,
+                  "frac": round(agg_bytes / (st_ms["aggregate"] / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+                  "traffic": measured_traffic(args.config, "aggregate"),
+                  "l2_gather_bytes": B * H * N * K * (C // H) * es}
     total_flops = proj_f + sim_f + conv_f
     if train:
         # backward: twice the projection and conv GEMM work plus the sparse
@@ -568,12 +619,14 @@ def main():
                                f"H={H} K={K} {metric} {conv} sampling={sampling}",
                    "B": B, "N": N, "C": C, "H": H, "K": K, "sampling": sampling},
         "roofline": roof,
+        "gather_stage": gather,
+        "stage_roofline": stage_roof,
         "layer": {"flops": total_flops, "tflops": round(layer_tflops, 2),
                   "frac_of_mfma_peak": round(layer_tflops / peak_mfma, 4)},
         "stages_ms": {k_: round(v_, 4) for k_, v_ in st_ms.items()},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(rec), flush=True)
+    return rec
 
 
 if __name__ == "__main__":
