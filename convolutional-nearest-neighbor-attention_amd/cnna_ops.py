@@ -27,6 +27,7 @@ ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_OPTION, ERR_K_RANGE, ERR_SEQ, ERR_WS, ERR_GR
     -1, -2, -3, -4, -5, -6, -7, -8, -9)
 ERR_SCRATCH = -10
 NOALLOC_SCRATCH_BYTES = 128 << 20    # CNNA_NOALLOC_SCRATCH_BYTES
+STAT_TILE = 128                      # CNNA_STAT_TILE: columns per row-statistics partial
 
 
 class Desc(ctypes.Structure):
@@ -48,6 +49,13 @@ class Grads(ctypes.Structure):
     """Mirror of ``cnna_grads``."""
 
     _fields_ = [(n, ctypes.c_void_p) for n in ("dx", "dWq", "dWk", "dWv", "dconv_w0", "dconv_w1")]
+
+
+class Ln(ctypes.Structure):
+    """Mirror of ``cnna_ln``: a LayerNorm folded into the GEMM that loads its rows."""
+
+    _fields_ = [("stats", ctypes.c_void_p), ("gamma", ctypes.c_void_p), ("beta", ctypes.c_void_p),
+                ("eps", ctypes.c_float)]
 
 
 def _load():
@@ -78,6 +86,10 @@ def _load():
                                 ctypes.POINTER(Grads), P, ctypes.c_size_t, P], I32),
         "cnna_layernorm": ([I32, I64, I32, P, I64, P, I64, P, I64, P, P, ctypes.c_float, P, I64, P], I32),
         "cnna_linear": ([I32, I64, I32, I32, P, I64, P, P, I32, P, I64, P, I64, P], I32),
+        "cnna_row_stats": ([I32, I64, I32, P, I64, P, P], I32),
+        "cnna_linear_ln": ([I32, I64, I32, I32, P, I64, ctypes.POINTER(Ln), P, P, I32, P, I64, P, I64, P, P],
+                           I32),
+        "cnna_project_qkv_ln": ([D, P, I64, ctypes.POINTER(Ln), P, P, P, P, P, P, P, P, P, P], I32),
         "cnna_conv1d_branch_workspace": ([I32] * 6, ctypes.c_size_t),
         "cnna_conv1d_branch": ([I32] * 6 + [P, I64, P, P, P, P, P, P, P, I64, P, ctypes.c_size_t, P], I32),
     }
@@ -88,7 +100,7 @@ def _load():
     return lib
 
 
-ABI_VERSION = 3        # CNNA_ABI_VERSION of the include/cnna.h this binding mirrors
+ABI_VERSION = 4        # CNNA_ABI_VERSION of the include/cnna.h this binding mirrors
 LIB = _load()
 if LIB.cnna_abi_version() != ABI_VERSION:
     raise ImportError(f"libcnna.so ABI {LIB.cnna_abi_version()} != {ABI_VERSION}: rebuild it with "
@@ -98,6 +110,7 @@ EXPORTED = ("cnna_abi_version", "cnna_error_string", "cnna_check_desc", "cnna_he
             "cnna_output_proj", "cnna_forward_workspace", "cnna_forward", "cnna_forward_noalloc",
             "cnna_output_proj_backward_workspace", "cnna_output_proj_backward",
             "cnna_core_backward_workspace", "cnna_core_backward", "cnna_layernorm", "cnna_linear",
+            "cnna_row_stats", "cnna_linear_ln", "cnna_project_qkv_ln",
             "cnna_conv1d_branch_workspace", "cnna_conv1d_branch")
 ACT_NONE, ACT_GELU = 0, 1
 
@@ -166,8 +179,11 @@ def _out_rows(out: torch.Tensor, B: int, N: int, C: int) -> int:
     return out.stride(1)
 
 
-def project_qkv(d: Desc, x: torch.Tensor, cand: Optional[torch.Tensor], Wq, Wk, Wv):
-    """Returns q (BH,Nq,dkp), k, v (BH,N,dkp), qn, kn (euclidean norms or None)."""
+def project_qkv(d: Desc, x: torch.Tensor, cand: Optional[torch.Tensor], Wq, Wk, Wv, ln=None):
+    """Returns q (BH,Nq,dkp), k, v (BH,N,dkp), qn, kn (euclidean norms or None).
+
+    ``ln``: a :class:`FoldedNorm` of x's rows; the projections then run on
+    LayerNorm(x), normalised as the GEMM loads x (inference only)."""
     x = _token_rows(x)
     ldx = x.stride(1)
     BH, dkp = d.B * d.H, head_stride(d)
@@ -179,9 +195,15 @@ def project_qkv(d: Desc, x: torch.Tensor, cand: Optional[torch.Tensor], Wq, Wk, 
         # euclidean distances need the norms; the cosine backward needs them too
         qn = torch.empty((BH * d.Nq,), dtype=torch.float32, device=x.device)
         kn = torch.empty((BH * d.N,), dtype=torch.float32, device=x.device)
-    check(LIB.cnna_project_qkv(ctypes.byref(d), _ptr(x), ldx, _ptr(cand), _ptr(Wq.contiguous()),
-                               _ptr(Wk.contiguous()), _ptr(Wv.contiguous()), _ptr(q), _ptr(k),
-                               _ptr(v), _ptr(qn), _ptr(kn), _stream()))
+    if ln is None:
+        check(LIB.cnna_project_qkv(ctypes.byref(d), _ptr(x), ldx, _ptr(cand), _ptr(Wq.contiguous()),
+                                   _ptr(Wk.contiguous()), _ptr(Wv.contiguous()), _ptr(q), _ptr(k),
+                                   _ptr(v), _ptr(qn), _ptr(kn), _stream()))
+    else:
+        ln.check(x)
+        check(LIB.cnna_project_qkv_ln(ctypes.byref(d), _ptr(x), ldx, ctypes.byref(ln.struct()), _ptr(cand),
+                                      _ptr(Wq.contiguous()), _ptr(Wk.contiguous()), _ptr(Wv.contiguous()),
+                                      _ptr(q), _ptr(k), _ptr(v), _ptr(qn), _ptr(kn), _stream()))
     return q, k, v, qn, kn
 
 
@@ -279,18 +301,90 @@ def layernorm(x, weight, bias, eps, residual=None, want_sum=False):
     return y
 
 
-def linear(a, W, bias=None, gelu=False, residual=None):
+def linear(a, W, bias=None, gelu=False, residual=None, ln=None, want_stats=False):
     """act(a @ W^T + bias) + residual through the MFMA GEMM (nn.Linear with the
-    ViT block's epilogues fused: vit.py:253-257, 263-264, 269); no autograd."""
+    ViT block's epilogues fused: vit.py:253-257, 263-264, 269); no autograd.
+
+    ``ln``: a :class:`FoldedNorm` of a's rows; the GEMM then runs on
+    LayerNorm(a), normalised as it loads a.  ``want_stats``: also return the
+    row-statistics partials of the output (a :class:`FoldedNorm` without its
+    module), from the GEMM's epilogue where the library supports it (bf16,
+    aligned rows), else from a statistics pass over the output."""
     ar = _rows(a)
     M, Kd = ar.shape
     Nout = W.shape[0]
     rr = None if residual is None else _rows(residual)
     out = torch.empty((M, Nout), dtype=a.dtype, device=a.device)
-    check(LIB.cnna_linear(dtype_code(a.dtype), M, Nout, Kd, _ptr(ar), ar.stride(0), _ptr(W.contiguous()),
-                          _ptr(None if bias is None else bias.contiguous()), ACT_GELU if gelu else ACT_NONE,
-                          _ptr(rr), 0 if rr is None else rr.stride(0), _ptr(out), out.stride(0), _stream()))
-    return out.view(*a.shape[:-1], Nout)
+    epi = want_stats and _stats_epilogue_ok(out, rr)
+    st = torch.empty((M, stat_parts(Nout), 2), dtype=torch.float32, device=a.device) if epi else None
+    lns = None
+    if ln is not None:
+        ln.check(ar)
+        lns = ln.struct()
+    check(LIB.cnna_linear_ln(dtype_code(a.dtype), M, Nout, Kd, _ptr(ar), ar.stride(0),
+                             None if lns is None else ctypes.byref(lns), _ptr(W.contiguous()),
+                             _ptr(None if bias is None else bias.contiguous()), ACT_GELU if gelu else ACT_NONE,
+                             _ptr(rr), 0 if rr is None else rr.stride(0), _ptr(out), out.stride(0), _ptr(st),
+                             _stream()))
+    out = out.view(*a.shape[:-1], Nout)
+    if not want_stats:
+        return out
+    return out, (FoldedNorm(st, M, Nout) if epi else row_stats(out))
+
+
+def stat_parts(C: int) -> int:
+    """CNNA_STAT_PARTS(C): row-statistics partials per row of C columns."""
+    return (C + STAT_TILE - 1) // STAT_TILE
+
+
+def _stats_epilogue_ok(out: torch.Tensor, rr: Optional[torch.Tensor]) -> bool:
+    """The GEMM's statistics epilogue applies (bf16, Nout % 8 == 0, 16-byte
+    aligned rows); otherwise the statistics come from ``row_stats``."""
+    if out.dtype != torch.bfloat16 or out.shape[1] % 8 or out.data_ptr() % 16 or out.stride(0) % 8:
+        return False
+    return rr is None or (rr.data_ptr() % 16 == 0 and rr.stride(0) % 8 == 0)
+
+
+class FoldedNorm:
+    """A LayerNorm split for folding: the fp32 statistics partials of ``rows``
+    rows of ``C`` columns ((rows, stat_parts(C), 2): each 128-column tile's
+    mean and sum of squared deviations), and, once ``with_norm`` names it, the
+    nn.LayerNorm whose normalisation the consuming GEMM applies."""
+
+    def __init__(self, stats: torch.Tensor, rows: int, C: int, weight=None, bias=None, eps=1e-5):
+        self.stats, self.rows, self.C = stats, rows, C
+        self.weight, self.bias, self.eps = weight, bias, float(eps)
+
+    def with_norm(self, norm: torch.nn.LayerNorm) -> "FoldedNorm":
+        if tuple(norm.normalized_shape) != (self.C,):
+            raise ValueError(f"cnna: LayerNorm over {tuple(norm.normalized_shape)} folded into rows of {self.C}")
+        return FoldedNorm(self.stats, self.rows, self.C, norm.weight, norm.bias, norm.eps)
+
+    def check(self, rows2d: torch.Tensor) -> None:
+        n = rows2d.numel() // rows2d.shape[-1]
+        if n != self.rows or rows2d.shape[-1] != self.C:
+            raise ValueError(f"cnna: statistics of {self.rows} x {self.C} rows for a {n} x {rows2d.shape[-1]} "
+                             "operand")
+        for p in (self.weight, self.bias):
+            if p is not None and p.dtype != rows2d.dtype:
+                raise TypeError(f"cnna: LayerNorm parameters in {p.dtype} for {rows2d.dtype} rows")
+
+    def struct(self) -> Ln:
+        g = None if self.weight is None else self.weight.contiguous()
+        b = None if self.bias is None else self.bias.contiguous()
+        self._keep = (g, b)     # alive until the launch has been queued
+        return Ln(self.stats.data_ptr(), None if g is None else g.data_ptr(),
+                  None if b is None else b.data_ptr(), self.eps)
+
+
+def row_stats(x: torch.Tensor) -> FoldedNorm:
+    """Statistics partials of the rows of ``x`` (..., C) for a LayerNorm folded
+    into the GEMM that consumes x (the pre-pass of the first block)."""
+    xr = _rows(x)
+    rows, C = xr.shape
+    st = torch.empty((rows, stat_parts(C), 2), dtype=torch.float32, device=x.device)
+    check(LIB.cnna_row_stats(dtype_code(x.dtype), rows, C, _ptr(xr), xr.stride(0), _ptr(st), _stream()))
+    return FoldedNorm(st, rows, C)
 
 
 def conv1d_branch(x, Wx, bx, conv_w, conv_b, Wo, bo, num_heads, out=None):

@@ -145,18 +145,6 @@ __global__ __launch_bounds__(256) void unmerge_tile_kernel(const T* dz, T* dy, i
 }
 
 // ------------------------------------------------------------------ tok_bwd
-template <int CTRL>
-CNNA_DEV float dpp_f(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
-}
-// sum over the 16 lanes of a DPP row (every lane gets the row's sum)
-CNNA_DEV float row16_sum(float v) {
-  v += dpp_f<0xB1>(v);    // quad_perm [1, 0, 3, 2]
-  v += dpp_f<0x4E>(v);    // quad_perm [2, 3, 0, 1]
-  v += dpp_f<0x141>(v);   // row_half_mirror
-  v += dpp_f<0x140>(v);   // row_mirror
-  return v;
-}
 
 // sum over groups of N lanes (N = 8 or 16) inside a DPP row
 template <int N>

@@ -7,7 +7,8 @@
 // rstd = 1/sqrt(var + eps) as nn.LayerNorm.  Rows of 16-byte vectors: 16 lanes
 // per row with DPP reductions; otherwise one wave per row, element by element.
 // With a residual the sum is rounded to the storage type first (the unfused
-// x + y produces that tensor) and optionally written out.
+// x + y produces that tensor) and optionally written out.  A statistics-only
+// kernel writes the per-tile partials a folded LayerNorm (gemm.hip) reads.
 #include "common.h"
 #include "kernels.h"
 
@@ -73,17 +74,6 @@ __global__ __launch_bounds__(256) void layernorm_kernel(LnArgs a) {
 // Vector form: 16 lanes per row (4 rows per wave), 16-byte vectors; lane g of
 // a row holds vectors g, g + 16, ... (EV per lane).  The row sums are DPP
 // reductions inside the 16-lane row (no LDS traffic).
-template <int CTRL>
-CNNA_DEV float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
-}
-CNNA_DEV float row16_sum(float v) {
-  v += dpp<0xB1>(v);    // quad_perm [1, 0, 3, 2]
-  v += dpp<0x4E>(v);    // quad_perm [2, 3, 0, 1]
-  v += dpp<0x141>(v);   // row_half_mirror
-  v += dpp<0x140>(v);   // row_mirror
-  return v;
-}
 
 template <typename T, int EV>
 __global__ __launch_bounds__(256) void layernorm_vec_kernel(LnArgs a) {
@@ -160,6 +150,29 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(LnArgs a) {
   }
 }
 
+// Statistics only, for a LayerNorm folded into the GEMM that consumes its
+// output: per ROW_STAT_TILE-column tile of each row, the tile's mean and M2
+// (the sum of squared deviations from that mean), two passes.  One wave per
+// row, two columns per lane per tile.
+template <typename T>
+__global__ __launch_bounds__(256) void row_stats_kernel(LnArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const T* x = static_cast<const T*>(a.x) + row * a.ldx;
+  const int parts = (a.C + ROW_STAT_TILE - 1) / ROW_STAT_TILE;
+  for (int t = 0; t < parts; ++t) {
+    const int c0 = t * ROW_STAT_TILE, nt = min(ROW_STAT_TILE, a.C - c0);
+    const bool k0 = lane < nt, k1 = lane + 64 < nt;
+    const float v0 = k0 ? ldf(x + c0 + lane) : 0.0f;
+    const float v1 = k1 ? ldf(x + c0 + 64 + lane) : 0.0f;
+    const float mean = wave_sum(v0 + v1) / (float)nt;
+    const float d0 = k0 ? v0 - mean : 0.0f, d1 = k1 ? v1 - mean : 0.0f;
+    const float q = wave_sum(d0 * d0 + d1 * d1);
+    if (lane == 0) *reinterpret_cast<float2*>(a.stats + (row * parts + t) * 2) = make_float2(mean, q);
+  }
+}
+
 inline bool a16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 template <typename T>
@@ -199,6 +212,16 @@ int launch_ln_t(const LnArgs& a, hipStream_t s) {
 int launch_layernorm(int dtype, const LnArgs& a, hipStream_t s) {
   if (a.rows <= 0) return 0;
   if (a.C <= 0) return CNNA_ERR_SHAPE;
+  if (a.stats != nullptr) {
+    const dim3 grid((unsigned)((a.rows + 3) / 4));
+    if (dtype == CNNA_BF16)
+      hipLaunchKernelGGL(row_stats_kernel<uint16_t>, grid, dim3(256), 0, s, a);
+    else if (dtype == CNNA_F32)
+      hipLaunchKernelGGL(row_stats_kernel<float>, grid, dim3(256), 0, s, a);
+    else
+      return CNNA_ERR_DTYPE;
+    return (int)hipGetLastError();
+  }
   if (dtype == CNNA_BF16) return launch_ln_t<uint16_t>(a, s);
   if (dtype == CNNA_F32) return launch_ln_t<float>(a, s);
   return CNNA_ERR_DTYPE;

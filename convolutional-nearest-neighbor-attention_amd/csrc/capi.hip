@@ -12,6 +12,8 @@
 
 using namespace cnna_desc_util;
 
+static_assert(CNNA_STAT_TILE == ROW_STAT_TILE, "statistics tile of the ABI and the kernels");
+
 extern "C" {
 
 int cnna_abi_version(void) { return CNNA_ABI_VERSION; }
@@ -33,7 +35,9 @@ const char* cnna_error_string(int code) {
     case CNNA_ERR_UNSUPPORTED:
       return "cnna: configuration not supported by this build (limits: K <= 32 neighbours, "
              "head width d_k (+1 with coordinate encoding) <= 256 for bfloat16 and <= 128 for "
-             "float32, at most 65536 candidates)";
+             "float32, at most 65536 candidates; folded LayerNorm: C <= 1024; row statistics "
+             "epilogue: bfloat16, Nout % 8 == 0, 16-byte aligned out / res with row strides that "
+             "are multiples of 8 elements)";
     default: break;
   }
   if (code > 0) return hipGetErrorString((hipError_t)code);
@@ -64,7 +68,24 @@ int cnna_check_desc(const cnna_desc* d) {
 
 int cnna_head_stride(const cnna_desc* d) { return d ? dkp_of(d) : 0; }
 
-int cnna_project_qkv(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* cand,
+}  // extern "C"
+
+namespace {
+
+// LayerNorm prologue of a GEMM over Kd-channel rows (NULL: none)
+int set_ln(GemmArgs& g, const cnna_ln* ln) {
+  if (ln == nullptr) return CNNA_OK;
+  if (!ln->stats) return CNNA_ERR_NULL;
+  if (((uintptr_t)ln->stats & 3) != 0) return CNNA_ERR_SHAPE;
+  g.ln_stats = ln->stats;
+  g.ln_parts = (g.Kd + ROW_STAT_TILE - 1) / ROW_STAT_TILE;
+  g.ln_gamma = ln->gamma;
+  g.ln_beta = ln->beta;
+  g.ln_eps = ln->eps;
+  return CNNA_OK;
+}
+
+int project_qkv_impl(const cnna_desc* d, const void* x, int64_t ldx, const cnna_ln* ln, const int32_t* cand,
                      const void* Wq, const void* Wk, const void* Wv, void* q, void* k, void* v,
                      float* qn, float* kn, void* stream) {
   int st = cnna_check_desc(d);
@@ -88,6 +109,7 @@ int cnna_project_qkv(const cnna_desc* d, const void* x, int64_t ldx, const int32
   g.o_dkp = dkp;
   g.avec = ((ldx * es) % 16 == 0) && aligned16(x);
   g.bvec = ((d->C * es) % 16 == 0) && aligned16(Wq) && aligned16(Wk) && aligned16(Wv);
+  if ((st = set_ln(g, ln))) return st;
   if (!d->sampled) {
     // one launch: [Q | K | V] = x @ [Wq; Wk; Wv]^T
     g.M = d->B * d->N;
@@ -132,6 +154,23 @@ int cnna_project_qkv(const cnna_desc* d, const void* x, int64_t ldx, const int32
     if ((st = launch_prep(d->dtype, p, s))) return st;
   }
   return CNNA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cnna_project_qkv(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* cand,
+                     const void* Wq, const void* Wk, const void* Wv, void* q, void* k, void* v,
+                     float* qn, float* kn, void* stream) {
+  return project_qkv_impl(d, x, ldx, nullptr, cand, Wq, Wk, Wv, q, k, v, qn, kn, stream);
+}
+
+int cnna_project_qkv_ln(const cnna_desc* d, const void* x, int64_t ldx, const cnna_ln* ln,
+                        const int32_t* cand, const void* Wq, const void* Wk, const void* Wv, void* q,
+                        void* k, void* v, float* qn, float* kn, void* stream) {
+  if (!ln) return CNNA_ERR_NULL;
+  return project_qkv_impl(d, x, ldx, ln, cand, Wq, Wk, Wv, q, k, v, qn, kn, stream);
 }
 
 int cnna_select(const cnna_desc* d, const void* k, const void* q, const float* kn, const float* qn,
@@ -287,9 +326,33 @@ int cnna_layernorm(int32_t dtype, int64_t rows, int32_t C, const void* x, int64_
   return launch_layernorm(dtype, a, (hipStream_t)stream);
 }
 
+int cnna_row_stats(int32_t dtype, int64_t rows, int32_t C, const void* x, int64_t ldx, float* stats,
+                   void* stream) {
+  if (dtype != CNNA_F32 && dtype != CNNA_BF16) return CNNA_ERR_DTYPE;
+  if (rows < 0 || C <= 0 || ldx < C) return CNNA_ERR_SHAPE;
+  if (rows == 0) return 0;
+  if (!x || !stats) return CNNA_ERR_NULL;
+  if (((uintptr_t)stats & 7) != 0) return CNNA_ERR_SHAPE;
+  LnArgs a;
+  memset(&a, 0, sizeof(a));
+  a.x = x;
+  a.ldx = ldx;
+  a.rows = rows;
+  a.C = C;
+  a.stats = stats;
+  return launch_layernorm(dtype, a, (hipStream_t)stream);
+}
+
 int cnna_linear(int32_t dtype, int64_t M, int32_t Nout, int32_t Kd, const void* a, int64_t lda,
                 const void* W, const void* bias, int32_t act, const void* res, int64_t ldr, void* out,
                 int64_t ldo, void* stream) {
+  return cnna_linear_ln(dtype, M, Nout, Kd, a, lda, nullptr, W, bias, act, res, ldr, out, ldo, nullptr,
+                        stream);
+}
+
+int cnna_linear_ln(int32_t dtype, int64_t M, int32_t Nout, int32_t Kd, const void* a, int64_t lda,
+                   const cnna_ln* ln, const void* W, const void* bias, int32_t act, const void* res,
+                   int64_t ldr, void* out, int64_t ldo, float* stats_out, void* stream) {
   if (dtype != CNNA_F32 && dtype != CNNA_BF16) return CNNA_ERR_DTYPE;
   if (act != CNNA_ACT_NONE && act != CNNA_ACT_GELU) return CNNA_ERR_OPTION;
   if (M < 0 || M > INT32_MAX || Nout <= 0 || Kd <= 0 || lda < Kd || ldo < Nout || (res && ldr < Nout))
@@ -314,6 +377,10 @@ int cnna_linear(int32_t dtype, int64_t M, int32_t Nout, int32_t Kd, const void* 
   g.act = act == CNNA_ACT_GELU ? GEMM_ACT_GELU : GEMM_ACT_NONE;
   g.res = res;
   g.ldr = ldr;
+  int st = set_ln(g, ln);
+  if (st) return st;
+  if (stats_out != nullptr && ((uintptr_t)stats_out & 7) != 0) return CNNA_ERR_SHAPE;
+  g.st_out = stats_out;
   return launch_gemm(dtype, GEMM_A_ROWS, GEMM_O_PLAIN, g, (hipStream_t)stream);
 }
 

@@ -99,6 +99,20 @@ CNNA_DEV float gelu_erf(float x) {
   return 0.5f * x * (x >= 0.0f ? 2.0f - erfc : erfc);
 }
 
+// Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), every lane gets
+// it; no LDS traffic.  All 16 lanes must be active.
+template <int CTRL>
+CNNA_DEV float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+CNNA_DEV float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+  v += dpp_f<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+  v += dpp_f<0x141>(v);   // row_half_mirror
+  v += dpp_f<0x140>(v);   // row_mirror
+  return v;
+}
+
 CNNA_DEV int mfma_row(int v, int lane) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
 
 // Map a linear block id so that consecutive work items land on the same XCD

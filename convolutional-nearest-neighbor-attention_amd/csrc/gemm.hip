@@ -13,12 +13,23 @@
 // The next k-tile is fetched into registers while the current one is
 // multiplied from LDS (rows padded by 16 bytes).  Blocks are ordered so that
 // all column tiles of a row tile run on the same XCD (shared L2).
+//
+// LayerNorm folding (the pre-norm ViT block, vit.py:260-267): with a LN
+// prologue the A rows are normalised in registers between the global load and
+// the LDS store, from per-row statistics combined out of per-128-column
+// (mean, M2) partials; with a statistics epilogue the bf16 GEMM that writes a
+// residual-stream row (W_o + residual, fc2 + residual) also writes those
+// partials for the rows it stores, so the LayerNorm that follows costs no
+// pass of its own.
 #include "common.h"
 #include "kernels.h"
 
 namespace {
 
 constexpr int BM = 128, BN = 128;
+static_assert(BN == ROW_STAT_TILE, "one statistics partial per column tile");
+// widest row a LayerNorm prologue normalises (gamma / beta staged in LDS)
+constexpr int LN_MAX_K = 1024;
 
 template <typename T> struct GemmCfg;
 template <> struct GemmCfg<uint16_t> { static constexpr int BK = 64, VEC = 8; };
@@ -73,8 +84,9 @@ CNNA_DEV void store4(float* p, float a, float b, float c, float d) {
 // EPI: the nn.Linear extras of a plain output are compiled in (0: none, 1: bias
 // and residual, 2: bias, GELU and residual), as separate instances so the
 // operator's own GEMMs keep their epilogues lean
+// XF: bit 0 the LayerNorm prologue on A, bit 1 the row-statistics epilogue
 // (three blocks per CU: accumulators in AGPRs + VGPRs within 168 registers)
-template <typename T, int AMODE, int OMODE, bool FAST, int EPI = 0>
+template <typename T, int AMODE, int OMODE, bool FAST, int EPI = 0, int XF = 0>
 __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
   using M_ = Mfma<T>;
   constexpr int BK = GemmCfg<T>::BK, VEC = GemmCfg<T>::VEC;
@@ -84,6 +96,12 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) T smem_ab[(BM + BN) * LDS_STRIDE];
   T* As = smem_ab;
   T* Bs = smem_ab + BM * LDS_STRIDE;
+  // LayerNorm prologue: gamma, beta (fp32, zero past Kd) and each tile row's
+  // (mean, rstd), read back as the A tiles are stashed
+  __shared__ __attribute__((aligned(16))) float ln_smem[(XF & 1) ? 2 * LN_MAX_K + 2 * BM : 4];
+  float* ln_g = ln_smem;
+  float* ln_b = ln_smem + LN_MAX_K;
+  float* ln_row = ln_smem + 2 * LN_MAX_K;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -119,6 +137,39 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
     const int mat = wrow_ok[i] ? n / g.ncol_each : 0;
     const int rn = wrow_ok[i] ? n - mat * g.ncol_each : 0;
     wrow_ptr[i] = static_cast<const T*>(g.w[mat]) + (int64_t)rn * g.Kd;
+  }
+
+  if (XF & 1) {
+    // gamma / beta over the whole reduction (Kd <= LN_MAX_K, a multiple of BK)
+    const T* gp = static_cast<const T*>(g.ln_gamma);
+    const T* bp = static_cast<const T*>(g.ln_beta);
+    for (int c = tid; c < LN_MAX_K; c += 256) {
+      const bool in = c < g.Kd;
+      ln_g[c] = in ? (gp ? ldf(gp + c) : 1.0f) : 0.0f;
+      ln_b[c] = (in && bp) ? ldf(bp + c) : 0.0f;
+    }
+    // mean and 1/sqrt(var + eps) of tile row tid from the row's per-tile
+    // (mean, M2) partials (tile t holds min(ROW_STAT_TILE, Kd - t * ROW_STAT_TILE) columns)
+    if (tid < BM) {
+      const int m = min(m0 + tid, g.M - 1);
+      int64_t sr = m;
+      if (g.arow != nullptr) {
+        const int b = m / g.a_rows, rr = m - b * g.a_rows;
+        sr = (int64_t)b * g.a_src_rows + g.arow[rr];
+      }
+      const float* sp = g.ln_stats + sr * (2 * g.ln_parts);
+      float sm = 0.0f;
+      for (int t = 0; t < g.ln_parts; ++t) sm += (float)min(ROW_STAT_TILE, g.Kd - t * ROW_STAT_TILE) * sp[2 * t];
+      const float mean = sm / (float)g.Kd;
+      float q = 0.0f;
+      for (int t = 0; t < g.ln_parts; ++t) {
+        const float d = sp[2 * t] - mean;
+        q += sp[2 * t + 1] + (float)min(ROW_STAT_TILE, g.Kd - t * ROW_STAT_TILE) * d * d;
+      }
+      ln_row[2 * tid] = mean;
+      ln_row[2 * tid + 1] = 1.0f / sqrtf(q / (float)g.Kd + g.ln_eps);
+    }
+    __syncthreads();
   }
 
   Pack<T, VEC> ra[NV], rw[NV];
@@ -177,9 +228,32 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
       }
     }
   };
-  auto stash = [&]() __attribute__((always_inline)) {
+  auto stash = [&](int k0) __attribute__((always_inline)) {
+    float gv[(XF & 1) ? VEC : 1], bv[(XF & 1) ? VEC : 1];
+    if (XF & 1) {
+      // every vector of a thread covers the same columns (256 % VPR == 0)
+#pragma unroll
+      for (int t = 0; t < VEC; t += 4) {
+        const float4 g4 = *reinterpret_cast<const float4*>(&ln_g[k0 + kvv[0] + t]);
+        const float4 b4 = *reinterpret_cast<const float4*>(&ln_b[k0 + kvv[0] + t]);
+        gv[t] = g4.x; gv[t + 1] = g4.y; gv[t + 2] = g4.z; gv[t + 3] = g4.w;
+        bv[t] = b4.x; bv[t + 1] = b4.y; bv[t + 2] = b4.z; bv[t + 3] = b4.w;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
+      if (XF & 1) {
+        // (x - mean) * rstd * gamma + beta, rounded to T as nn.LayerNorm's output;
+        // columns past Kd stay zero
+        const float2 st = *reinterpret_cast<const float2*>(&ln_row[2 * rowv[i]]);
+#pragma unroll
+        for (int t = 0; t < VEC; ++t) {
+          float y = (ldf(&ra[i].e[t]) - st.x) * st.y;
+          y = y * gv[t] + bv[t];
+          if (!FAST && k0 + kvv[i] + t >= g.Kd) y = 0.0f;
+          stf(&ra[i].e[t], y);
+        }
+      }
       *reinterpret_cast<u32x4_t*>(&As[rowv[i] * LDS_STRIDE + kvv[i]]) = ra[i].u;
       *reinterpret_cast<u32x4_t*>(&Bs[rowv[i] * LDS_STRIDE + kvv[i]]) = rw[i].u;
     }
@@ -197,7 +271,7 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
 
   fetch(0);
   for (int k0 = 0; k0 < g.Kd; k0 += BK) {
-    stash();
+    stash(k0);
     __syncthreads();
     if (k0 + BK < g.Kd) fetch(k0 + BK);
 #pragma unroll
@@ -288,6 +362,9 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
       r = m - b * g.o_rows;
     }
     T* obase = static_cast<T*>(g.o[OMODE == GEMM_O_HEADSPLIT ? (mat > 2 ? 2 : mat) : 0]);
+    // statistics epilogue: the 16 threads of a row segment are one DPP row
+    const int st_parts = (g.Nc + ROW_STAT_TILE - 1) / ROW_STAT_TILE;
+    const float st_inv = 1.0f / (float)min(BN, g.Nc - n0);
 #pragma unroll
     for (int it = 0; it < (BM * BN / 8) / 256; ++it) {
       const int ml = (tid >> 4) + it * 16;
@@ -298,6 +375,45 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
           r -= g.o_rows;
           ++b;
         }
+      }
+      if (XF & 2) {
+        // plain output, Nc % 8 == 0 (so every segment in range is whole): store
+        // the row segment, then (mean, M2) of the row's stored values in this
+        // column tile, two passes over registers
+        const bool ok = m < g.M && n < g.Nc;
+        u32x4_t val = {0u, 0u, 0u, 0u};
+        if (ok) {
+          val = *reinterpret_cast<const u32x4_t*>(&Cs[ml * CP + nl]);
+          if (EPI && g.res != nullptr) {
+            const u32x4_t rv = *reinterpret_cast<const u32x4_t*>(static_cast<const T*>(g.res) + (int64_t)m * g.ldr + n);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              val[q] = f2bf2(__uint_as_float(val[q] << 16) + __uint_as_float(rv[q] << 16),
+                             __uint_as_float(val[q] & 0xffff0000u) + __uint_as_float(rv[q] & 0xffff0000u));
+          }
+          *reinterpret_cast<u32x4_t*>(obase + (int64_t)m * g.ldo + n) = val;
+        }
+        float xv[8], sm = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          xv[2 * q] = __uint_as_float(val[q] << 16);
+          xv[2 * q + 1] = __uint_as_float(val[q] & 0xffff0000u);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) sm += xv[u];
+        const float mean = row16_sum(sm) * st_inv;
+        float sq = 0.0f;
+        if (ok) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const float d = xv[u] - mean;
+            sq += d * d;
+          }
+        }
+        sq = row16_sum(sq);
+        if ((tid & 15) == 0 && m < g.M)
+          *reinterpret_cast<float2*>(g.st_out + ((int64_t)m * st_parts + n0 / ROW_STAT_TILE) * 2) = make_float2(mean, sq);
+        continue;
       }
       if (m >= g.M || n >= g.Nc) continue;
       u32x4_t val = *reinterpret_cast<const u32x4_t*>(&Cs[ml * CP + nl]);
@@ -410,8 +526,47 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
 }
 
 template <typename T, bool FAST>
+int launch_x(int omode, const GemmArgs& g, hipStream_t s, dim3 grid) {
+  // LayerNorm prologue and / or statistics epilogue (row-major A)
+  const int xf = (g.ln_stats ? 1 : 0) | (g.st_out ? 2 : 0);
+  if (omode == GEMM_O_HEADSPLIT) {
+    if (xf != 1 || g.bias || g.res || g.act != GEMM_ACT_NONE) return CNNA_ERR_OPTION;
+    hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_HEADSPLIT, FAST, 0, 1>), grid, dim3(256), 0, s, g);
+    return (int)hipGetLastError();
+  }
+  const bool gelu = g.act == GEMM_ACT_GELU;
+  if (xf == 1) {
+    if (gelu)
+      hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN, FAST, 2, 1>), grid, dim3(256), 0, s, g);
+    else
+      hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN, FAST, 1, 1>), grid, dim3(256), 0, s, g);
+    return (int)hipGetLastError();
+  }
+  if constexpr (sizeof(T) == 2) {
+    // the statistics come from the staged bf16 epilogue
+    if (!g.ostage || g.Nc % 8 != 0) return CNNA_ERR_UNSUPPORTED;
+    if (gelu && xf == 2)
+      hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN, FAST, 2, 2>), grid, dim3(256), 0, s, g);
+    else if (gelu)
+      hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN, FAST, 2, 3>), grid, dim3(256), 0, s, g);
+    else if (xf == 2)
+      hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN, FAST, 1, 2>), grid, dim3(256), 0, s, g);
+    else
+      hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN, FAST, 1, 3>), grid, dim3(256), 0, s, g);
+    return (int)hipGetLastError();
+  } else {
+    return CNNA_ERR_UNSUPPORTED;
+  }
+}
+
+template <typename T, bool FAST>
 int launch_f(int amode, int omode, const GemmArgs& g, hipStream_t s) {
   dim3 grid(((g.Nc + BN - 1) / BN) * ((g.M + BM - 1) / BM));
+  if (g.ln_stats || g.st_out) {
+    if (amode != GEMM_A_ROWS) return CNNA_ERR_OPTION;
+    if (g.ln_stats && g.Kd > LN_MAX_K) return CNNA_ERR_UNSUPPORTED;
+    return launch_x<T, FAST>(omode, g, s, grid);
+  }
   if (amode == GEMM_A_ROWS && omode == GEMM_O_HEADSPLIT)
     hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_HEADSPLIT, FAST>), grid, dim3(256), 0, s, g);
   else if (amode == GEMM_A_ROWS && omode == GEMM_O_PLAIN && g.act == GEMM_ACT_GELU)

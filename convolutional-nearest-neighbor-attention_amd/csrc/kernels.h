@@ -37,8 +37,23 @@ struct GemmArgs {
   int act;           // GEMM_ACT_*
   const void* res;   // (M, Nc) residual with row stride ldr, or NULL
   int64_t ldr;
+  // prologue (bf16, row-major A): A rows are LayerNorm-ed on load,
+  //   a[m][k] = round((x[m][k] - mean_m) * rstd_m * gamma[k] + beta[k]),
+  // mean_m / rstd_m combined from ln_parts per-tile (mean, M2) partials of
+  // the row (ROW_STAT_TILE columns each, the last one partial), or NULL
+  const float* ln_stats;
+  int ln_parts;
+  const void* ln_gamma;
+  const void* ln_beta;
+  float ln_eps;
+  // epilogue (staged bf16, plain output): per ROW_STAT_TILE-column tile of
+  // each output row, (mean, M2) of the stored values, at
+  // st_out[(m * ceil(Nc / ROW_STAT_TILE) + tile) * 2], or NULL
+  float* st_out;
 };
 enum { GEMM_ACT_NONE = 0, GEMM_ACT_GELU = 1 };
+// columns per row-statistics partial (the GEMM's column tile)
+constexpr int ROW_STAT_TILE = 128;
 
 int launch_gemm(int dtype, int amode, int omode, const GemmArgs& g, hipStream_t s);
 
@@ -58,6 +73,10 @@ struct LnArgs {
   int64_t ldy;
   int64_t rows;
   int C;
+  // statistics only: y unused, (mean, M2) of each row over ROW_STAT_TILE
+  // column tiles written to stats[(row * parts + t) * 2] (the GEMM
+  // prologue's format), or NULL
+  float* stats;
 };
 int launch_layernorm(int dtype, const LnArgs& a, hipStream_t s);
 

@@ -143,6 +143,30 @@ class MultiHeadConvNNAttention(nn.Module):
         z = ops.ConvNNCore.apply(x, Wq, Wk, Wv, w0, w1, cand, d, True)
         return self._conv_output_dropout(z), d
 
+    def core_folded(self, x, ln):
+        """``core`` of LayerNorm(x) in inference with the LayerNorm folded into
+        the Q/K/V projection (vit.py:262 feeding layers.py:264-265): ``ln``
+        (cnna_ops.FoldedNorm) holds x's row statistics and the norm, and the
+        projection GEMM normalises x as it loads it.  Eval mode: no autograd,
+        dropout is the identity.  Returns (z, desc)."""
+        if self.training:
+            raise RuntimeError("MultiHeadConvNNAttention.core_folded is an inference path (eval mode)")
+        B, N, C = x.shape
+        self.batch_size = B                                                          # layers.py:239
+        cand = self._candidates(x)
+        Nq = N if cand is None else int(cand.numel())
+        d = ops.make_desc(B, N, C, self.num_heads, Nq, self.K, self.seq_length, x.dtype,
+                          self.magnitude_type, self.convolution_type, self.softmax_topk_val,
+                          cand is not None, self.coordinate_encoding)
+        if self.W_q.weight.dtype != x.dtype:
+            raise RuntimeError(f"mat1 and mat2 must have the same dtype, but got {x.dtype} and "
+                               f"{self.W_q.weight.dtype}")
+        w0, w1 = self._conv_weights()
+        q, k, v, qn, kn = ops.project_qkv(d, x, cand, self.W_q.weight, self.W_k.weight, self.W_v.weight,
+                                          ln=ln)
+        idx, _, w, _ = ops.select_cols(d, k, q, kn, qn, cand)
+        return ops.aggregate(d, v, idx, w, w0, w1), d
+
     def _conv_output_dropout(self, z):
         """``self.dropout`` on the conv output y (B*H, d_k, N), where the reference
         applies it (layers.py:316), given the head-merged z (B, N, C).

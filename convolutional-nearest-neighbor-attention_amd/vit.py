@@ -11,11 +11,16 @@ operator on a channel slice beside a Conv1d or softmax-attention branch),
 ``Attention``; the reference's Local / Neighborhood / Sparse attention
 families are outside this operator's scope and raise ValueError.
 
-In inference (eval mode, no gradients, no autocast, not being traced) each
-block runs with its prologue and epilogues fused: LayerNorm kernels, W_o +
-residual (ConvNN attention) or the
-residual add inside the second LayerNorm (other layers), fc1 + bias + GELU and
-fc2 + bias + residual in the GEMM epilogues (cnna_layernorm, cnna_linear).
+In inference (eval mode, no gradients, no autocast, not being traced) the
+blocks run with their prologues and epilogues fused.  With ConvNN attention
+both LayerNorms are folded: the GEMM that writes a residual-stream row (W_o +
+residual, fc2 + residual) also writes the row's statistics in its epilogue
+(bf16; fp32 takes a statistics pass over the row instead), and the GEMM that
+consumes the row (the next block's Q/K/V projection, fc1) normalises it as it
+loads it; the first block's statistics come from a pre-pass (cnna_row_stats,
+cnna_linear_ln, cnna_project_qkv_ln).  Other layers keep a LayerNorm kernel in
+front of the attention and the residual add inside the second LayerNorm.
+fc1 + bias + GELU and fc2 + bias + residual are GEMM epilogues throughout.
 Training and autograd use the composable modules.
 """
 from __future__ import annotations
@@ -124,7 +129,7 @@ class TransformerEncoder(nn.Module):
 
     def forward(self, x):
         if self._fusable(x):
-            return self._forward_fused(x)
+            return self._forward_fused(x)[0]
         x = x + self.dropout1(self.attention(self.norm1(x)))
         return x + self.dropout2(self.mlp(self.norm2(x)))
 
@@ -136,22 +141,36 @@ class TransformerEncoder(nn.Module):
             return False
         return self.norm1.weight.dtype == x.dtype
 
-    def _forward_fused(self, x):
-        """The same block with its prologue and epilogues fused: LayerNorm
-        kernels, W_o with the residual add in its epilogue, fc1 with bias + GELU
-        and fc2 with bias + residual in theirs."""
+    def _foldable(self, x):
+        return (isinstance(self.attention, MultiHeadConvNNAttention) and x.shape[-1] <= 1024
+                and self.mlp[0].in_features == x.shape[-1])
+
+    def _forward_fused(self, x, stats=None):
+        """The same block with its prologue and epilogues fused.  Returns the
+        block output and, with ConvNN attention, its row statistics
+        (cnna_ops.FoldedNorm) for the next block's folded norm1; ``stats``:
+        those of x from the previous block (computed here when None).
+
+        ConvNN attention: norm1 folded into the Q/K/V projection, W_o with the
+        residual add and the statistics of x1 = x + attention in its epilogue,
+        norm2 folded into fc1 (bias + GELU epilogue), fc2 with bias + residual
+        and the output's statistics in its epilogue.  Other layers: LayerNorm
+        kernel, the layer, the residual add fused into norm2, fc1 and fc2 with
+        their epilogues."""
         fc1, fc2 = self.mlp[0], self.mlp[3]
+        if self._foldable(x):
+            if stats is None:
+                stats = ops.row_stats(x)
+            z, _ = self.attention.core_folded(x, stats.with_norm(self.norm1))
+            x1, st1 = ops.linear(z, self.attention.W_o.weight, residual=x, want_stats=True)
+            m = ops.linear(x1, fc1.weight, fc1.bias, gelu=True, ln=st1.with_norm(self.norm2))
+            return ops.linear(m, fc2.weight, fc2.bias, residual=x1, want_stats=True)
         h = ops.layernorm(x, self.norm1.weight, self.norm1.bias, self.norm1.eps)
-        if isinstance(self.attention, MultiHeadConvNNAttention):
-            z, _ = self.attention.core(h)
-            x1 = ops.linear(z, self.attention.W_o.weight, residual=x)
-            h2 = ops.layernorm(x1, self.norm2.weight, self.norm2.bias, self.norm2.eps)
-        else:
-            a = self.attention(h)
-            h2, x1 = ops.layernorm(a, self.norm2.weight, self.norm2.bias, self.norm2.eps, residual=x,
-                                   want_sum=True)
+        a = self.attention(h)
+        h2, x1 = ops.layernorm(a, self.norm2.weight, self.norm2.bias, self.norm2.eps, residual=x,
+                               want_sum=True)
         m = ops.linear(h2, fc1.weight, fc1.bias, gelu=True)
-        return ops.linear(m, fc2.weight, fc2.bias, residual=x1)
+        return ops.linear(m, fc2.weight, fc2.bias, residual=x1), None
 
 
 class ViT(nn.Module):
@@ -174,5 +193,12 @@ class ViT(nn.Module):
 
     def forward(self, x):
         x = self.positional_encoding(self.patch_embedding(x))
-        x = self.transformer_encoder(x)
+        blocks = self.transformer_encoder
+        if len(blocks) and blocks[0]._fusable(x):
+            # fused inference: each block hands its output's row statistics on
+            stats = None
+            for blk in blocks:
+                x, stats = blk._forward_fused(x, stats)
+        else:
+            x = blocks(x)
         return self.classifier(x[:, 0])

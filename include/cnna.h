@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define CNNA_ABI_VERSION 3
+#define CNNA_ABI_VERSION 4
 
 enum cnna_dtype { CNNA_F32 = 0, CNNA_BF16 = 1 };
 /* magnitude_type (layers.py:167-168, 323-340) */
@@ -255,6 +255,52 @@ int cnna_layernorm(int32_t dtype, int64_t rows, int32_t C, const void* x, int64_
 int cnna_linear(int32_t dtype, int64_t M, int32_t Nout, int32_t Kd, const void* a, int64_t lda,
                 const void* W, const void* bias, int32_t act, const void* res, int64_t ldr, void* out,
                 int64_t ldo, void* stream);
+
+/* LayerNorm folded into the GEMM that consumes it (the pre-norm block,
+ * vit.py:260-267: norm1 -> attention's W_q/W_k/W_v, norm2 -> fc1).
+ * nn.LayerNorm's two steps are split between two kernels:
+ *  - the statistics, written by the kernel that produces the rows: the
+ *    statistics epilogue of cnna_linear_ln (W_o + residual, fc2 + residual)
+ *    or, for the first block, cnna_row_stats;
+ *  - the normalisation (x - mean) / sqrt(var + eps) * gamma + beta, rounded to
+ *    the dtype as nn.LayerNorm's output is, applied by the consuming GEMM
+ *    (cnna_linear_ln, cnna_project_qkv_ln) as it loads each row.
+ * The statistics are fp32 partials, stats[(row * CNNA_STAT_PARTS(C) + t) * 2
+ * + {0, 1}] = the mean and the sum of squared deviations from that mean of the
+ * row's columns [128 t, min(128 (t + 1), C)); mean and var (biased, as
+ * nn.LayerNorm) of the row are combined from them. */
+#define CNNA_STAT_TILE 128
+#define CNNA_STAT_PARTS(C) (((C) + CNNA_STAT_TILE - 1) / CNNA_STAT_TILE)
+
+typedef struct cnna_ln {
+  const float* stats;   /* partials of the GEMM's A rows (indexed by A row) */
+  const void* gamma;    /* (C) LayerNorm weight, or NULL (1) */
+  const void* beta;     /* (C) LayerNorm bias, or NULL (0) */
+  float eps;
+} cnna_ln;
+
+/* Statistics partials of x (rows, C) row stride ldx into stats (8-byte
+ * aligned, rows * CNNA_STAT_PARTS(C) * 2 floats). */
+int cnna_row_stats(int32_t dtype, int64_t rows, int32_t C, const void* x, int64_t ldx, float* stats,
+                   void* stream);
+
+/* cnna_linear with the LayerNorm of a folded in (ln; C = Kd) and, when
+ * stats_out is not NULL, the statistics partials of the stored out rows
+ * ((M, CNNA_STAT_PARTS(Nout), 2), 8-byte aligned).  The statistics epilogue
+ * needs bfloat16, Nout % 8 == 0 and 16-byte aligned out / res with row strides
+ * that are multiples of 8 elements (else CNNA_ERR_UNSUPPORTED).  ln may be
+ * NULL (no prologue). */
+int cnna_linear_ln(int32_t dtype, int64_t M, int32_t Nout, int32_t Kd, const void* a, int64_t lda,
+                   const cnna_ln* ln, const void* W, const void* bias, int32_t act, const void* res,
+                   int64_t ldr, void* out, int64_t ldo, float* stats_out, void* stream);
+
+/* cnna_project_qkv on LayerNorm(x) (vit.py:262 feeding layers.py:264-265):
+ * the rows of x are normalised with ln (C = d->C; stats indexed by the row
+ * b * N + t of x, also for the sampled Q rows) as the projection GEMM loads
+ * them.  ln is required. */
+int cnna_project_qkv_ln(const cnna_desc* d, const void* x, int64_t ldx, const cnna_ln* ln,
+                        const int32_t* cand, const void* Wq, const void* Wk, const void* Wv, void* q,
+                        void* k, void* v, float* qn, float* kn, void* stream);
 
 /* ---- branching callers (layers.py:502-652) ----
  * MultiHeadConv1dAttention (layers.py:452-499), the Conv1d branch of

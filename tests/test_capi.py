@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert ops.LIB.cnna_abi_version() == 3
+    assert ops.LIB.cnna_abi_version() == 4
 
 
 def desc(**kw):
@@ -157,3 +157,31 @@ def test_noalloc_scratch_limit():
                                       None, 768, None)
     assert st == ops.ERR_SCRATCH
     assert b"128 MiB" in ops.LIB.cnna_error_string(ops.ERR_SCRATCH)
+
+
+def test_folded_layernorm_limits():
+    """The LayerNorm folding entry points reject what their kernels do not do
+    before any device call: fp32 statistics epilogue, Nout % 8 != 0, rows
+    wider than 1024 for the prologue, misaligned statistics, a missing ln."""
+    fake = ctypes.c_void_p(1 << 20)              # never dereferenced: rejected first
+    st = ctypes.c_void_p(1 << 20)
+    ln = ops.Ln(1 << 20, None, None, 1e-5)
+    lin = ops.LIB.cnna_linear_ln
+    # fp32 output statistics come from cnna_row_stats, not the GEMM epilogue
+    assert lin(ops.CNNA_F32, 64, 192, 192, fake, 192, None, fake, None, 0, None, 0, fake, 192, st,
+               None) == ops.ERR_UNSUPPORTED
+    assert lin(ops.CNNA_BF16, 64, 196, 192, fake, 192, None, fake, None, 0, None, 0, fake, 196, st,
+               None) == ops.ERR_UNSUPPORTED
+    assert lin(ops.CNNA_BF16, 64, 192, 2048, fake, 2048, ctypes.byref(ln), fake, None, 0, None, 0, fake, 192,
+               None, None) == ops.ERR_UNSUPPORTED
+    assert lin(ops.CNNA_BF16, 64, 192, 192, fake, 192, None, fake, None, 0, None, 0, fake, 192,
+               ctypes.c_void_p((1 << 20) + 4), None) == ops.ERR_SHAPE
+    bad = ops.Ln(None, None, None, 1e-5)
+    assert lin(ops.CNNA_BF16, 64, 192, 192, fake, 192, ctypes.byref(bad), fake, None, 0, None, 0, fake, 192,
+               None, None) == ops.ERR_NULL
+    d = desc(dtype=ops.CNNA_BF16)
+    assert ops.LIB.cnna_project_qkv_ln(ctypes.byref(d), fake, 12, None, None, fake, fake, fake, fake, fake,
+                                       fake, None, None, None) == ops.ERR_NULL
+    assert ops.LIB.cnna_row_stats(ops.CNNA_BF16, 4, 192, fake, 100, st, None) == ops.ERR_SHAPE
+    assert ops.LIB.cnna_row_stats(ops.CNNA_BF16, 0, 192, None, 192, None, None) == 0
+    assert b"folded LayerNorm" in ops.LIB.cnna_error_string(ops.ERR_UNSUPPORTED)

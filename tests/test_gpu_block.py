@@ -5,7 +5,12 @@
 * cnna_linear's bias / GELU / residual epilogues equal the unfused
   nn.Linear -> nn.GELU -> + residual sequence;
 * a ViT whose blocks run fused (eval, no gradients) equals the same ViT run
-  through the composable modules.
+  through the composable modules;
+* the folded LayerNorm: cnna_row_stats's per-tile (mean, M2) partials equal
+  the float64 ones; the GEMMs' LayerNorm prologue equals LayerNorm -> GEMM
+  (cnna_linear_ln, cnna_project_qkv_ln, also on the sampled Q rows); the
+  statistics epilogue equals the statistics pass over the stored output; a
+  folded ViT block runs no LayerNorm kernel.
 """
 import copy
 
@@ -135,3 +140,168 @@ def test_patch_embedding_gemm_matches_conv(dtype):
         ref = pe(x).float().detach()                  # Conv2d + nn.LayerNorm
     tol = 1e-4 if dtype == torch.float32 else 3e-2
     torch.testing.assert_close(fused, ref, rtol=tol, atol=tol)
+
+
+# ---------------------------------------------------------------- folded LayerNorm
+def _tile_stats64(x):
+    """Float64 (mean, M2) of each 128-column tile of each row."""
+    x = x.double()
+    rows, C = x.shape
+    out = torch.zeros(rows, (C + 127) // 128, 2, dtype=torch.float64, device=x.device)
+    for t in range(out.shape[1]):
+        seg = x[:, 128 * t:min(C, 128 * t + 128)]
+        mu = seg.mean(1)
+        out[:, t, 0] = mu
+        out[:, t, 1] = ((seg - mu[:, None]) ** 2).sum(1)
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("C", [64, 192, 200, 768, 1000])
+def test_row_stats_partials(dtype, C):
+    torch.manual_seed(C)
+    base = (torch.randn(333, C + 8, device=DEV) * 2 + 3).to(dtype)
+    x = base[:, 4:4 + C]                              # row stride C + 8, offset start
+    st = ops.row_stats(x)
+    assert st.stats.shape == (333, (C + 127) // 128, 2) and st.rows == 333 and st.C == C
+    torch.testing.assert_close(st.stats.double(), _tile_stats64(x), rtol=1e-5, atol=1e-4)
+
+
+def _ln_ref(x, norm):
+    """nn.LayerNorm's output in x's dtype (fp32 statistics of the same x)."""
+    return F.layer_norm(x.float(), norm.normalized_shape, None if norm.weight is None else norm.weight.float(),
+                        None if norm.bias is None else norm.bias.float(), norm.eps).to(x.dtype)
+
+
+def _norm(C, dtype, affine=True, seed=0):
+    torch.manual_seed(seed)
+    n = torch.nn.LayerNorm(C, elementwise_affine=affine).to(DEV)
+    if affine:
+        with torch.no_grad():
+            n.weight.copy_(torch.rand(C) + 0.5)
+            n.bias.copy_(torch.randn(C) * 0.3)
+    return n.to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,Nout,Kd", [(1000, 768, 192), (1000, 192, 768), (257, 200, 200), (300, 136, 1000)])
+@pytest.mark.parametrize("mode", ["plain", "bias_gelu", "bias_res"])
+def test_linear_layernorm_prologue(dtype, M, Nout, Kd, mode):
+    """linear(ln=row statistics + norm) == linear(LayerNorm(a)): Kd % 64 == 0
+    takes the vector loader, 200 and 1000 the element-wise one."""
+    torch.manual_seed(M + Kd)
+    a = (torch.randn(M, Kd, device=DEV) * 1.5 + 0.7).to(dtype)
+    W = (torch.randn(Nout, Kd, device=DEV) / Kd ** 0.5).to(dtype)
+    bias = torch.randn(Nout, device=DEV).to(dtype) if mode.startswith("bias") else None
+    res = torch.randn(M, Nout, device=DEV).to(dtype) if mode.endswith("res") else None
+    norm = _norm(Kd, dtype, seed=Kd)
+    out = ops.linear(a, W, bias, gelu=mode == "bias_gelu", residual=res, ln=ops.row_stats(a).with_norm(norm))
+    h = _ln_ref(a, norm)
+    ref = ops.linear(h, W, bias, gelu=mode == "bias_gelu", residual=res)
+    if dtype == torch.float32:
+        torch.testing.assert_close(out, ref, rtol=1e-4, atol=1e-4)
+    else:
+        # h may differ by one bf16 ulp where the statistics' summation order
+        # moves a value across a rounding boundary
+        torch.testing.assert_close(out.float(), ref.float(), rtol=2e-2, atol=2e-2)
+        assert (out.float() - ref.float()).abs().mean() < 2e-3
+
+
+def test_linear_layernorm_prologue_without_affine():
+    torch.manual_seed(5)
+    a = torch.randn(500, 192, device=DEV) * 4 - 2
+    W = torch.randn(384, 192, device=DEV) / 14
+    norm = _norm(192, torch.float32, affine=False)
+    out = ops.linear(a, W, ln=ops.row_stats(a).with_norm(norm))
+    ref = F.linear(F.layer_norm(a, (192,)), W)
+    torch.testing.assert_close(out, ref, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("M,Nout,Kd", [(1000, 192, 192), (257, 200, 768), (25216, 192, 768), (64, 1024, 64)])
+@pytest.mark.parametrize("mode", ["plain", "bias_res", "res", "bias_gelu"])
+def test_linear_statistics_epilogue(M, Nout, Kd, mode):
+    """bf16: the epilogue's partials are those of the stored output rows (the
+    residual sum as rounded to bf16), and the output is unchanged."""
+    torch.manual_seed(M + Nout + Kd)
+    a = torch.randn(M, Kd, device=DEV).to(torch.bfloat16)
+    W = (torch.randn(Nout, Kd, device=DEV) / Kd ** 0.5).to(torch.bfloat16)
+    bias = torch.randn(Nout, device=DEV).to(torch.bfloat16) if mode.startswith("bias") else None
+    res = (torch.randn(M, Nout, device=DEV) * 3).to(torch.bfloat16) if mode.endswith("res") else None
+    out, st = ops.linear(a, W, bias, gelu=mode == "bias_gelu", residual=res, want_stats=True)
+    assert ops._stats_epilogue_ok(out.view(M, Nout), None if res is None else res)
+    ref = ops.linear(a, W, bias, gelu=mode == "bias_gelu", residual=res)
+    assert torch.equal(out, ref)
+    assert st.rows == M and st.C == Nout
+    torch.testing.assert_close(st.stats.double(), _tile_stats64(out), rtol=1e-5, atol=1e-4)
+
+
+def test_linear_statistics_fp32_from_pass():
+    """fp32 (no statistics epilogue): want_stats falls back to the statistics
+    pass over the output."""
+    torch.manual_seed(2)
+    a = torch.randn(300, 192, device=DEV)
+    W = torch.randn(192, 192, device=DEV) / 14
+    out, st = ops.linear(a, W, residual=a, want_stats=True)
+    torch.testing.assert_close(st.stats.double(), _tile_stats64(out), rtol=1e-5, atol=1e-4)
+
+
+def _qkv_desc(dtype, sampled, coord=False, metric="matmul", B=2, N=197, C=192, H=3, Nq=None):
+    Nq = N if not sampled else Nq
+    return ops.make_desc(B, N, C, H, Nq, 9, N, dtype, metric, "standard", True, sampled, coord)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", ["all", "sampled", "coord_cosine", "strided"])
+def test_project_qkv_layernorm_prologue(dtype, case):
+    """project_qkv(x, ln) == project_qkv(LayerNorm(x)); the sampled Q rows read
+    the statistics of their source rows x[b, cand]."""
+    torch.manual_seed(11)
+    B, N, C = 2, 197, 192
+    xb = (torch.randn(B, N, C + 64, device=DEV) * 2 - 1).to(dtype)
+    x = xb[..., :C] if case == "strided" else xb[..., :C].contiguous()
+    cand = None
+    if case == "sampled":
+        cand = torch.randperm(N, device=DEV)[:40].to(torch.int32)
+    d = _qkv_desc(dtype, case == "sampled", coord=case == "coord_cosine",
+                  metric="cosine" if case == "coord_cosine" else "matmul", Nq=40)
+    Wq, Wk, Wv = [(torch.randn(C, C, device=DEV) / C ** 0.5).to(dtype) for _ in range(3)]
+    norm = _norm(C, dtype, seed=1)
+    got = ops.project_qkv(d, x, cand, Wq, Wk, Wv, ln=ops.row_stats(x).with_norm(norm))
+    ref = ops.project_qkv(d, _ln_ref(x, norm), cand, Wq, Wk, Wv)
+    for g, r in zip(got, ref):
+        if r is None:
+            assert g is None
+            continue
+        if dtype == torch.float32:
+            torch.testing.assert_close(g, r, rtol=1e-4, atol=1e-4)
+        else:
+            torch.testing.assert_close(g.float(), r.float(), rtol=2e-2, atol=2e-2)
+
+
+def test_folded_vit_block_runs_no_layernorm_kernel(monkeypatch):
+    """With ConvNN attention both LayerNorms of a fused block are folded into
+    the GEMMs: the LayerNorm kernel is never called, the first block's
+    statistics come from one pre-pass and the others from the epilogues."""
+    model = _tiny_vit(torch.bfloat16)
+    imgs = torch.randn(4, 3, 64, 64, device=DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        expect = model(imgs)
+    calls = {"ln": 0, "stats": 0}
+    real_ln, real_stats = ops.layernorm, ops.row_stats
+
+    def ln_spy(*a, **k):
+        calls["ln"] += 1
+        return real_ln(*a, **k)
+
+    def stats_spy(*a, **k):
+        calls["stats"] += 1
+        return real_stats(*a, **k)
+
+    monkeypatch.setattr(ops, "layernorm", ln_spy)
+    monkeypatch.setattr(ops, "row_stats", stats_spy)
+    with torch.no_grad():
+        got = model(imgs)
+    assert torch.equal(got, expect)
+    assert calls["stats"] == 1
+    # the patch embedding's own LayerNorm (vit.py PatchEmbedding.norm) is the one kernel left
+    assert calls["ln"] == 1
