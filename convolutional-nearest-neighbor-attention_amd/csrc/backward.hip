@@ -443,7 +443,8 @@ int launch_tok_k(const TokBwdArgs& a, hipStream_t s) {
   if (a.K <= 9) return launch_tok_t<T, CPL, 9>(a, s);
   if (a.K <= 16) return launch_tok_t<T, CPL, 16>(a, s);
   if (a.K <= 32) return launch_tok_t<T, CPL, 32>(a, s);
-  return CNNA_ERR_K_RANGE;
+  if (a.K <= 64) return launch_tok_t<T, CPL, 64>(a, s);
+  return CNNA_ERR_UNSUPPORTED;
 }
 
 template <typename T>

@@ -33,8 +33,8 @@ const char* cnna_error_string(int code) {
       return "cnna: the call needs more intermediate memory than the 128 MiB static scratch of "
              "cnna_forward_noalloc; call cnna_forward with a workspace";
     case CNNA_ERR_UNSUPPORTED:
-      return "cnna: configuration not supported by this build (limits: K <= 32 neighbours, "
-             "head width d_k (+1 with coordinate encoding) <= 256 for bfloat16 and <= 128 for "
+      return "cnna: configuration not supported by this build (limits: K <= 64 neighbours in the "
+             "backward, head width d_k (+1 with coordinate encoding) <= 256 for bfloat16 and <= 128 for "
              "float32, at most 65536 candidates; folded LayerNorm: C <= 1024; row statistics "
              "epilogue: bfloat16, Nout % 8 == 0, 16-byte aligned out / res with row strides that "
              "are multiples of 8 elements)";
@@ -57,8 +57,7 @@ int cnna_check_desc(const cnna_desc* d) {
   if (d->merge != CNNA_MERGE_REFERENCE && d->merge != CNNA_MERGE_CONCAT) return CNNA_ERR_OPTION;
   if (d->scale != 0.0f && (d->metric != CNNA_MATMUL || !isfinite(d->scale))) return CNNA_ERR_OPTION;
   if (d->merge == CNNA_MERGE_REFERENCE && d->H > 1 && d->seq_length != d->N) return CNNA_ERR_SEQ_LENGTH;
-  // the reference accepts these; the kernels' register lists and tiles do not
-  if (ksel_of(d) > 32 || d->K > 32) return CNNA_ERR_UNSUPPORTED;
+  // the reference accepts these; the kernels' tiles do not
   const int dkp = dkp_of(d);
   if (d->dtype == CNNA_BF16 && dkp > 256) return CNNA_ERR_UNSUPPORTED;
   if (d->dtype == CNNA_F32 && dkp > 128) return CNNA_ERR_UNSUPPORTED;

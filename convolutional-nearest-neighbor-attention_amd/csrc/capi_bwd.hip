@@ -157,6 +157,8 @@ int cnna_core_backward(const cnna_desc* d, const void* x, int64_t ldx, const int
                        const cnna_grads* gr, void* ws, size_t ws_bytes, void* stream) {
   int st = cnna_check_desc(d);
   if (st) return st;
+  // the per-token backward holds a token's entries one per lane
+  if (d->K > 64) return CNNA_ERR_UNSUPPORTED;
   if (!x || !Wq || !Wk || !Wv || !conv_w0 || !sv || !dz || !gr || !ws) return CNNA_ERR_NULL;
   if (!sv->q || !sv->k || !sv->v || !sv->idx || !sv->vals || !sv->w) return CNNA_ERR_NULL;
   if (d->metric != CNNA_MATMUL && (!sv->qn || !sv->kn)) return CNNA_ERR_NULL;

@@ -107,6 +107,8 @@ struct SelArgs {
   int32_t* cols;     // sampled: (BH, N, K) candidate column of each entry (slot 0: Nq), or NULL
   int softmax;       // softmax_topk_val
   int BH, N, Nq, dkp, K, Ksel, rb_per_bh;
+  int kbase;         // entries (after the sampled self slot) chosen by earlier rounds of a
+                     // selection wider than one list; 0 for the first round
   float kscale;      // key = acc * kscale for dot metrics (raw keys: value = key * kscale, kscale > 0)
   int kneg;          // raw keys of a negative matmul scale: rank -k.q (the key rows are negated)
   float mask_key;    // key of the self-masked candidate (sampled)

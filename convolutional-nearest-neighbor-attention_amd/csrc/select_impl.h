@@ -37,6 +37,13 @@
 //     positions where both halves have consumed a prefix of the candidate
 //     indices, so a later candidate never ties its way in ahead of a listed
 //     one.  The list is written out with the neighbour weights.
+//
+// K wider than one list (KMAX = 32): rounds of at most 32 entries.  Round r
+// (EX) excludes every candidate that ranks at or before the last entry of
+// round r - 1 (compared as packed (key, index) pairs, so ties continue in index
+// order); that entry is handed over in the idx / vals slot round r fills first.
+// Pass 1 masks keys >= the excluded key (a superset, so tau stays a lower
+// bound).  The weights of all K entries are computed by a final row kernel.
 #pragma once
 #include <type_traits>
 
@@ -151,7 +158,7 @@ constexpr int queue_cap() {
   return !EXACT ? 12 : (fixed + 20 * 256 * 6 <= budget ? 20 : (fixed + 16 * 256 * 6 <= budget ? 16 : 12));
 }
 
-template <typename T, int NCH, bool EXACT, int KMAX, bool EUC, bool SMP>
+template <typename T, int NCH, bool EXACT, int KMAX, bool EUC, bool SMP, bool EX = false>
 __global__ __launch_bounds__(NT, (sel_min_blocks<NCH * (sizeof(T) == 2 ? 4 : 1), KMAX, EUC, SMP>()))
 void select_kernel(SelArgs a) {
   using M_ = Mfma<T>;
@@ -195,6 +202,15 @@ void select_kernel(SelArgs a) {
   if (RAW && a.kneg) {
 #pragma unroll
     for (int c = 0; c < NCH; ++c) kf[c] = M_::neg(kf[c]);
+  }
+  // a later round: the previous round's last entry (key, candidate index)
+  constexpr int OFF = SMP ? 1 : 0;
+  float ekey = 0.0f;
+  uint32_t ej = 0;
+  if (EX) {
+    const int64_t eo = ((int64_t)bh * a.N + tic) * a.K + OFF + a.kbase;
+    ekey = key_of_ord(__float_as_uint(a.vals[eo]));
+    ej = ~(uint32_t)a.idx[eo];
   }
   // wait for the key rows here, so the tile loop carries no vector-memory waits
   // ahead of its MFMAs (s_waitcnt vmcnt(0))
@@ -354,6 +370,7 @@ void select_kernel(SelArgs a) {
           const int jl = b * 32 + mfma_row(v, lane);
           key[v] = keyof(acc[b][v], buf, jl);
           if (decltype(MASKED)::value && j0 + jl >= a.Nq) key[v] = -INFINITY;
+          if (EX && key[v] >= ekey) key[v] = -INFINITY;   // (may drop a tie that is still eligible)
         }
         // keys here are finite or -inf (masked rows, negative euclidean d^2)
         if (every) {
@@ -437,6 +454,8 @@ void select_kernel(SelArgs a) {
           const int jl = b * 32 + mfma_row(v, lane);
           float key = keyof(acc[b][v], buf, jl);
           if (decltype(MASKED)::value && j0 + jl >= a.Nq) key = __builtin_nanf("");
+          // a later round: only candidates ranking after the previous round's last entry
+          if (EX && !(key < ekey || (key == ekey && (uint32_t)(j0 + jl) > ej))) key = __builtin_nanf("");
           // (slot <= QC - 1 here: a check precedes every QCHK elements)
           if (PRED_APPEND) {
             // store the passers only; element steps where no lane passes skip it
@@ -466,7 +485,6 @@ void select_kernel(SelArgs a) {
   }
 
   // ---------------- the token's list -> idx, vals, w (values kept in registers)
-  constexpr int OFF = SMP ? 1 : 0;
   constexpr int KO = KMAX + OFF;
   float vv[KO], wv[KO];
   int tk[KO];
@@ -510,21 +528,42 @@ void select_kernel(SelArgs a) {
       for (int r = 0; r < KO; ++r) wv[r] = EUC ? 1.0f / (vv[r] + 1e-8f) : vv[r];
     }
   }
+  // another round follows: hand this round's last entry over in the slot
+  // after this round's entries (its first slot)
+  const int nxt = OFF + a.kbase + a.Ksel;
+  if (nxt < a.K && half == 0 && tvalid) {
+    const uint64_t last = lst[(a.Ksel - 1) * TPB + slot];
+    const int64_t eo = ((int64_t)bh * a.N + ti) * a.K + nxt;
+    a.vals[eo] = __uint_as_float((uint32_t)(last >> 32));
+    a.idx[eo] = (int32_t)(uint32_t)last;
+  }
   // The block's tokens are consecutive, so each output is one contiguous run
-  // of nvalid * K values: staged through LDS (the queue region, free after the
-  // final drains) and stored by all threads with consecutive addresses.
+  // of nvalid * K values (one round: the whole rows): staged through LDS (the
+  // queue region, free after the final drains) and stored by all threads with
+  // consecutive addresses.  This round writes kw entries per token from column
+  // c0, register entries rs ...
   uint32_t* stg = qent;
   const int nvalid = min(TPB, a.N - rb * TPB);
+  const int rs = a.kbase == 0 ? 0 : OFF;
+  const int kw = a.kbase == 0 ? OFF + a.Ksel : a.Ksel;
+  const int c0 = a.kbase == 0 ? 0 : OFF + a.kbase;
   const int64_t obase = ((int64_t)bh * a.N + rb * TPB) * a.K;
   auto emit = [&](auto get, uint32_t* dst) __attribute__((always_inline)) {
     __syncthreads();
     if (half == 0 && tvalid) {
 #pragma unroll
       for (int r = 0; r < KO; ++r)
-        if (r < a.K) stg[slot * a.K + r] = get(r);
+        if (r >= rs && r < rs + kw) stg[slot * kw + r - rs] = get(r);
     }
     __syncthreads();
-    for (int e = tid; e < nvalid * a.K; e += NT) dst[obase + e] = stg[e];
+    if (kw == a.K) {
+      for (int e = tid; e < nvalid * kw; e += NT) dst[obase + e] = stg[e];
+    } else {
+      for (int e = tid; e < nvalid * kw; e += NT) {
+        const int t = e / kw;
+        dst[obase + (int64_t)t * a.K + c0 + (e - t * kw)] = stg[e];
+      }
+    }
   };
   emit([&](int r) { return (uint32_t)tk[r]; }, reinterpret_cast<uint32_t*>(a.idx));
   emit([&](int r) { return __float_as_uint(vv[r]); }, reinterpret_cast<uint32_t*>(a.vals));
@@ -532,7 +571,7 @@ void select_kernel(SelArgs a) {
   if (SMP && a.cols != nullptr) emit([&](int r) { return (uint32_t)cl[r]; }, reinterpret_cast<uint32_t*>(a.cols));
 }
 
-template <typename T, int NCH, bool EXACT, int KMAX>
+template <typename T, int NCH, bool EXACT, int KMAX, bool EX = false>
 int launch_k(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
   auto smem = [&](int qc) {
     return 2 * TJ * (a.dkp + SelCfg<T>::VEC) * sizeof(T) + 2 * TJ * (sizeof(float) + sizeof(int)) + 8 * sizeof(int) +
@@ -540,26 +579,66 @@ int launch_k(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
   };
   const dim3 grid(a.BH * a.rb_per_bh);
   if (!euclid && !sampled)
-    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, false, false>), grid, dim3(NT),
+    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, false, false, EX>), grid, dim3(NT),
                        smem(queue_cap<T, NCH, EXACT, KMAX, false, false>()), s, a);
   else if (!euclid && sampled)
-    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, false, true>), grid, dim3(NT),
+    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, false, true, EX>), grid, dim3(NT),
                        smem(queue_cap<T, NCH, EXACT, KMAX, false, true>()), s, a);
   else if (euclid && !sampled)
-    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, true, false>), grid, dim3(NT),
+    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, true, false, EX>), grid, dim3(NT),
                        smem(queue_cap<T, NCH, EXACT, KMAX, true, false>()), s, a);
   else
-    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, true, true>), grid, dim3(NT),
+    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, true, true, EX>), grid, dim3(NT),
                        smem(queue_cap<T, NCH, EXACT, KMAX, true, true>()), s, a);
+  return (int)hipGetLastError();
+}
+
+// Neighbour weights of whole rows after a multi-round selection (the same
+// formulas as the single-round kernel: layers.py:352-355, 382-385, 394-397,
+// 426-429); one thread per token row.
+__global__ __launch_bounds__(256) void sel_weights_kernel(const float* vals, float* w, int64_t rows, int K,
+                                                          int softmax, int euclid) {
+  const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (row >= rows) return;
+  const float* v = vals + row * K;
+  float* o = w + row * K;
+  if (softmax) {
+    float mx = -INFINITY;
+    for (int r = 0; r < K; ++r) mx = fmaxf(mx, euclid ? -v[r] : v[r]);
+    float sum = 0.0f;
+    for (int r = 0; r < K; ++r) sum += expf((euclid ? -v[r] : v[r]) - mx);
+    for (int r = 0; r < K; ++r) o[r] = expf((euclid ? -v[r] : v[r]) - mx) / sum;
+  } else {
+    for (int r = 0; r < K; ++r) o[r] = euclid ? 1.0f / (v[r] + 1e-8f) : v[r];
+  }
+}
+
+// one list of KMAX entries, or rounds of 32 for wider selections
+template <typename T, int NCH, bool EXACT>
+int launch_rounds(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
+  if (EXACT && a.Ksel <= 9) return launch_k<T, NCH, EXACT, 9>(euclid, sampled, a, s);
+  if (EXACT && a.Ksel <= 16) return launch_k<T, NCH, EXACT, 16>(euclid, sampled, a, s);
+  if (a.Ksel <= 32) return launch_k<T, NCH, EXACT, 32>(euclid, sampled, a, s);
+  SelArgs r = a;
+  r.w = nullptr;
+  for (int base = 0; base < a.Ksel; base += 32) {
+    r.kbase = base;
+    r.Ksel = min(32, a.Ksel - base);
+    const int st = base == 0 ? launch_k<T, NCH, EXACT, 32, false>(euclid, sampled, r, s)
+                             : launch_k<T, NCH, EXACT, 32, true>(euclid, sampled, r, s);
+    if (st) return st;
+  }
+  if (a.w != nullptr) {
+    const int64_t rows = (int64_t)a.BH * a.N;
+    hipLaunchKernelGGL(sel_weights_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, a.vals, a.w,
+                       rows, a.K, a.softmax, euclid);
+  }
   return (int)hipGetLastError();
 }
 
 template <typename T, int NCH>
 int launch_n(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
-  if (a.Ksel <= 9) return launch_k<T, NCH, true, 9>(euclid, sampled, a, s);
-  if (a.Ksel <= 16) return launch_k<T, NCH, true, 16>(euclid, sampled, a, s);
-  if (a.Ksel <= 32) return launch_k<T, NCH, true, 32>(euclid, sampled, a, s);
-  return CNNA_ERR_K_RANGE;
+  return launch_rounds<T, NCH, true>(euclid, sampled, a, s);
 }
 
 template <typename T>
@@ -575,9 +654,8 @@ int launch_select_t(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
   if (nch == q) return launch_n<T, q>(euclid, sampled, a, s);
   if (nch == 2 * q) return launch_n<T, 2 * q>(euclid, sampled, a, s);
   if (nch == 4 * q) return launch_n<T, 4 * q>(euclid, sampled, a, s);
-  // other widths: guarded chunks, list of 32
-  if (a.Ksel > 32) return CNNA_ERR_K_RANGE;
-  return launch_k<T, SelCfg<T>::MAXCH, false, 32>(euclid, sampled, a, s);
+  // other widths: guarded chunks, lists of 32
+  return launch_rounds<T, SelCfg<T>::MAXCH, false>(euclid, sampled, a, s);
 }
 
 }  // namespace

@@ -432,7 +432,8 @@ class MultiHeadKvtAttention(nn.Module):
     head layout; forward and backward both run natively.  ``attn_drop`` draws
     the reference's dense (B, H, N, N) mask and applies it at the kept
     probabilities (the dropped entries of the reference's dense row are zero
-    already).  Native limits: ``topk`` <= 32 and no ``qkv_bias``
+    already).  Any ``topk`` runs forward (selections wider than 32 in rounds
+    of 32); the backward takes ``topk`` <= 64; ``qkv_bias`` is not supported
     (NotImplementedError otherwise).
     """
 
@@ -470,8 +471,6 @@ class MultiHeadKvtAttention(nn.Module):
         H = self.num_heads
         if self.topk > N:
             raise RuntimeError("selected index k out of range")                # torch.topk
-        if self.topk > 32:
-            raise NotImplementedError("cnna: MultiHeadKvtAttention supports topk <= 32")
         x, W, P = _amp_inputs(x, self.qkv.weight, self.proj.weight)
         if W.dtype != x.dtype:
             raise RuntimeError(f"mat1 and mat2 must have the same dtype, but got {x.dtype} and "

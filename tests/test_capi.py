@@ -64,7 +64,6 @@ def test_check_desc_ok():
     (dict(seq_length=197), ops.ERR_SEQ),               # H > 1 and seq_length != N
     (dict(K=0), ops.ERR_K_RANGE),
     # valid for the reference, beyond the kernels' limits: NotImplementedError, not a range error
-    (dict(N=64, Nq=64, seq_length=64, K=33), ops.ERR_UNSUPPORTED),
     (dict(C=3 * 264, dtype=ops.CNNA_BF16), ops.ERR_UNSUPPORTED),   # bf16 head width > 256
     (dict(C=3 * 136), ops.ERR_UNSUPPORTED),                        # f32 head width > 128
     (dict(N=70000, Nq=70000, seq_length=70000), ops.ERR_UNSUPPORTED),
@@ -98,7 +97,7 @@ def test_error_strings_and_exception_types():
         ops.check(ops.ERR_GROUPS)
     with pytest.raises(TypeError):
         ops.check(ops.ERR_DTYPE)
-    with pytest.raises(NotImplementedError, match="K <= 32"):
+    with pytest.raises(NotImplementedError, match="K <= 64"):
         ops.check(ops.ERR_UNSUPPORTED)
     assert b"workspace" in ops.LIB.cnna_error_string(ops.ERR_WS)
 
@@ -185,3 +184,18 @@ def test_folded_layernorm_limits():
     assert ops.LIB.cnna_row_stats(ops.CNNA_BF16, 4, 192, fake, 100, st, None) == ops.ERR_SHAPE
     assert ops.LIB.cnna_row_stats(ops.CNNA_BF16, 0, 192, None, 192, None, None) == 0
     assert b"folded LayerNorm" in ops.LIB.cnna_error_string(ops.ERR_UNSUPPORTED)
+
+
+def test_wide_k_forward_accepted_backward_limited():
+    """K > 32 runs forward (rounds of 32 in the select kernel); the backward
+    holds a token's entries one per lane and refuses K > 64 before any device
+    call (NotImplementedError naming the limit)."""
+    assert status(N=200, Nq=200, seq_length=200, K=100) == 0
+    assert status(N=200, Nq=200, seq_length=200, K=200) == 0
+    d = desc(N=200, Nq=200, seq_length=200, K=65)
+    fake = ctypes.c_void_p(1 << 20)
+    sv, gr = ops.Saved(*([1 << 20] * 10)), ops.Grads(*([1 << 20] * 6))
+    st = ops.LIB.cnna_core_backward(ctypes.byref(d), fake, 12, None, fake, fake, fake, fake, None,
+                                    ctypes.byref(sv), fake, ctypes.byref(gr), fake, 1 << 30, None)
+    assert st == ops.ERR_UNSUPPORTED
+    assert b"K <= 64" in ops.LIB.cnna_error_string(ops.ERR_UNSUPPORTED)

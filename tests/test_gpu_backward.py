@@ -107,6 +107,10 @@ BWD_EXTRA = [
     ("dk128_std_k16", dict(d_hidden=256, num_heads=2, K=16, convolution_type="standard", seq_length=64), 1, 64),
     # depthwise with 20-channel heads: the vector weight-gradient path (fp32, 5 vectors per row)
     ("matmul_dw_dk20", dict(d_hidden=60, num_heads=3, K=7, seq_length=45), 2, 45),
+    # K above one select list (rounds of 32) up to the backward's 64
+    ("k48_dw_dk64", dict(d_hidden=128, num_heads=2, K=48, seq_length=90), 2, 90),
+    ("k64_std_dk32", dict(d_hidden=64, num_heads=2, K=64, convolution_type="standard", seq_length=100), 1, 100),
+    ("k40_random_cosine_dws", dict(d_hidden=64, num_heads=2, K=40, sampling_type="random", num_samples=60, magnitude_type="cosine", convolution_type="depthwise-separable", seq_length=80), 2, 80),
 ]
 
 
@@ -117,7 +121,7 @@ def test_backward_fp32_more(name, kw, B, N):
 
 @pytest.mark.parametrize("conv,N,C,K", [("standard", 512, 768, 16), ("depthwise", 1024, 384, 9),
                                         ("depthwise", 256, 768, 32), ("depthwise", 197, 192, 9),
-                                        ("depthwise", 64, 60, 7)])
+                                        ("depthwise", 64, 60, 7), ("depthwise", 197, 192, 64)])
 def test_backward_bf16(conv, N, C, K):
     """bf16 at config-5 / config-3 / ViT head sizes (batch reduced); 20-channel
     heads take the element-wise weight-gradient path (rows not whole 16-byte

@@ -171,7 +171,9 @@ def _kvt_oracle(m, x, wmul=None):
 @pytest.mark.parametrize("B,N,C,H,topk,qs", [(8, 197, 192, 3, 9, None), (4, 256, 128, 1, 16, None),
                                              (3, 100, 96, 2, 1, 0.3), (2, 40, 64, 4, 32, None),
                                              (3, 100, 96, 2, 5, -0.3),
-                                             (2, 12, 48, 3, 12, None)])
+                                             (2, 12, 48, 3, 12, None),
+                                             # the reference's default topk=100 (rounds of 32)
+                                             (2, 197, 192, 3, 100, None), (2, 80, 64, 2, 50, 0.2)])
 def test_kvt_forward_matches_oracle(dtype, B, N, C, H, topk, qs):
     m = _kvt(dtype, C, H, topk, qk_scale=qs)
     x = torch.randn(B, N, C, device=DEV).to(dtype)
@@ -208,21 +210,25 @@ def test_kvt_errors():
     m = _kvt(torch.float32, 64, 2, topk=50)
     with pytest.raises(RuntimeError, match="out of range"):
         m(torch.randn(1, 20, 64, device=DEV))
-    with pytest.raises(NotImplementedError):
-        m(torch.randn(1, 60, 64, device=DEV))
+    # topk above 64: the forward runs, the backward is beyond the native limit
+    m = _kvt(torch.float32, 64, 2, topk=80).train()
+    x = torch.randn(1, 100, 64, device=DEV, requires_grad=True)
+    y = m(x)
+    with pytest.raises(NotImplementedError, match="K <= 64"):
+        y.sum().backward()
     with pytest.raises(NotImplementedError):
         MultiHeadKvtAttention(64, 2, qkv_bias=True, topk=4).to(DEV)(torch.randn(1, 8, 64, device=DEV))
 
 
-@pytest.mark.parametrize("H", [1, 3])
-def test_kvt_backward_matches_oracle(H):
-    m = _kvt(torch.float32, 96, H, topk=9).train()
+@pytest.mark.parametrize("H,topk", [(1, 9), (3, 9), (3, 48), (2, 64)])
+def test_kvt_backward_matches_oracle(H, topk):
+    m = _kvt(torch.float32, 96, H, topk=topk).train()
     x = torch.randn(3, 197, 96, device=DEV, requires_grad=True)
     m(x).square().sum().backward()
     xc = x.detach().double().cpu().requires_grad_(True)
     Wqkv = m.qkv.weight.detach().double().cpu().requires_grad_(True)
     Wp = m.proj.weight.detach().double().cpu().requires_grad_(True)
-    O.kvt(xc, Wqkv, Wp, H, 9, m.scale).square().sum().backward()
+    O.kvt(xc, Wqkv, Wp, H, topk, m.scale).square().sum().backward()
     torch.testing.assert_close(x.grad.double().cpu(), xc.grad, rtol=2e-3, atol=2e-3)
     torch.testing.assert_close(m.qkv.weight.grad.double().cpu(), Wqkv.grad, rtol=2e-3, atol=2e-3)
     torch.testing.assert_close(m.proj.weight.grad.double().cpu(), Wp.grad, rtol=2e-3, atol=2e-3)

@@ -269,3 +269,64 @@ def test_module_errors_match_reference():
     m = MultiHeadConvNNAttention(12, 3, 0.0, 17, "all", -1, 0, "matmul", seq_length=16).to(DEV)
     with pytest.raises(RuntimeError):
         m(torch.randn(2, 16, 12, device=DEV))
+
+
+# --------------------------------------------------------------------------- K wider than one list
+
+WIDE_K_CASES = [
+    # (name, cfg kwargs, B, N, dtype): K > 32 runs the select kernel in rounds of 32
+    ("k33_f32", dict(d_hidden=64, num_heads=2, K=33, seq_length=120), 2, 120, torch.float32),
+    ("k64_bf16_N1024", dict(d_hidden=384, num_heads=3, K=64, seq_length=1024), 1, 1024, torch.bfloat16),
+    ("k100_bf16_vit", dict(d_hidden=192, num_heads=3, K=100, seq_length=197), 2, 197, torch.bfloat16),
+    ("k197_eq_n_f32", dict(d_hidden=192, num_heads=3, K=197, seq_length=197), 1, 197, torch.float32),
+    ("k70_random_euclid_f32", dict(d_hidden=64, num_heads=2, K=70, sampling_type="random", num_samples=90, magnitude_type="euclidean", seq_length=150), 2, 150, torch.float32),
+    ("k41_spatial_cosine_f32", dict(d_hidden=96, num_heads=2, K=41, sampling_type="spatial", num_samples=60, magnitude_type="cosine", seq_length=100), 2, 100, torch.float32),
+    # d_k = 48: no exact-width instance, the guarded-chunk kernel in rounds
+    ("k45_dk48_bf16", dict(d_hidden=96, num_heads=2, K=45, seq_length=300), 2, 300, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("name,kw,B,N,dtype", WIDE_K_CASES, ids=[c[0] for c in WIDE_K_CASES])
+def test_select_wide_k(name, kw, B, N, dtype):
+    cfg = O.Config(**kw)
+    p, x = make(cfg, B, N, dtype, seed=5)
+    cand = cand_for(cfg, N)
+    d, r = run_stages(cfg, p, x, cand)
+    check_select(cfg, r, cand, B)
+    # the weights of all K entries (written after the last round)
+    v = r["vals"].double()
+    if cfg.softmax_topk_val:
+        exp_w = torch.softmax(-v if cfg.magnitude_type == "euclidean" else v, dim=-1)
+    else:
+        exp_w = 1.0 / (v + 1e-8) if cfg.magnitude_type == "euclidean" else v
+    torch.testing.assert_close(r["w"].double(), exp_w, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("K", [33, 50, 64, 70])
+def test_select_wide_k_ties_continue_in_index_order(K):
+    """Every key ties except one: the rounds must hand the tie over at the
+    32-entry boundary and continue with the next lowest index."""
+    cfg = O.Config(d_hidden=16, num_heads=1, K=K, seq_length=100)
+    B, N = 1, 100
+    d = desc_for(cfg, B, N, N, torch.float32)
+    k = torch.zeros(1, N, 16)
+    k[..., 0] = 1.0
+    q = torch.zeros(1, N, 16)
+    q[..., 0] = 0.5
+    q[0, 40, 0] = 0.75
+    idx, vals, w = ops.select(d, k.to(DEV), q.to(DEV))
+    torch.cuda.synchronize()
+    exp = [40] + [j for j in range(N) if j != 40][:K - 1]
+    assert (idx.cpu()[0] == torch.tensor(exp, dtype=torch.int32)).all()
+    assert torch.all(vals.cpu()[0, :, 1:] == 0.5 / 4.0)
+
+
+WIDE_K_E2E = [
+    ("k40_dw_f32", dict(d_hidden=96, num_heads=3, K=40, seq_length=100), 2, 100),
+    ("k36_std_random_f32", dict(d_hidden=64, num_heads=2, K=36, sampling_type="random", num_samples=50, convolution_type="standard", seq_length=80), 2, 80),
+]
+
+
+@pytest.mark.parametrize("name,kw,B,N", WIDE_K_E2E, ids=[c[0] for c in WIDE_K_E2E])
+def test_forward_wide_k_end_to_end(name, kw, B, N):
+    test_forward_fp32_end_to_end(name, kw, B, N)
