@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
   T* As = smem_ab;
   T* Bs = smem_ab + BM * LDS_STRIDE;
   // LayerNorm prologue: gamma, beta (fp32, zero past Kd) and each tile row's
-  // (mean, rstd), read back as the A tiles are stashed
+  // (rstd, -mean * rstd), read back as the A tiles are stashed
   __shared__ __attribute__((aligned(16))) float ln_smem[(XF & 1) ? 2 * LN_MAX_K + 2 * BM : 4];
   float* ln_g = ln_smem;
   float* ln_b = ln_smem + LN_MAX_K;
@@ -137,39 +137,6 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
     const int mat = wrow_ok[i] ? n / g.ncol_each : 0;
     const int rn = wrow_ok[i] ? n - mat * g.ncol_each : 0;
     wrow_ptr[i] = static_cast<const T*>(g.w[mat]) + (int64_t)rn * g.Kd;
-  }
-
-  if (XF & 1) {
-    // gamma / beta over the whole reduction (Kd <= LN_MAX_K, a multiple of BK)
-    const T* gp = static_cast<const T*>(g.ln_gamma);
-    const T* bp = static_cast<const T*>(g.ln_beta);
-    for (int c = tid; c < LN_MAX_K; c += 256) {
-      const bool in = c < g.Kd;
-      ln_g[c] = in ? (gp ? ldf(gp + c) : 1.0f) : 0.0f;
-      ln_b[c] = (in && bp) ? ldf(bp + c) : 0.0f;
-    }
-    // mean and 1/sqrt(var + eps) of tile row tid from the row's per-tile
-    // (mean, M2) partials (tile t holds min(ROW_STAT_TILE, Kd - t * ROW_STAT_TILE) columns)
-    if (tid < BM) {
-      const int m = min(m0 + tid, g.M - 1);
-      int64_t sr = m;
-      if (g.arow != nullptr) {
-        const int b = m / g.a_rows, rr = m - b * g.a_rows;
-        sr = (int64_t)b * g.a_src_rows + g.arow[rr];
-      }
-      const float* sp = g.ln_stats + sr * (2 * g.ln_parts);
-      float sm = 0.0f;
-      for (int t = 0; t < g.ln_parts; ++t) sm += (float)min(ROW_STAT_TILE, g.Kd - t * ROW_STAT_TILE) * sp[2 * t];
-      const float mean = sm / (float)g.Kd;
-      float q = 0.0f;
-      for (int t = 0; t < g.ln_parts; ++t) {
-        const float d = sp[2 * t] - mean;
-        q += sp[2 * t + 1] + (float)min(ROW_STAT_TILE, g.Kd - t * ROW_STAT_TILE) * d * d;
-      }
-      ln_row[2 * tid] = mean;
-      ln_row[2 * tid + 1] = 1.0f / sqrtf(q / (float)g.Kd + g.ln_eps);
-    }
-    __syncthreads();
   }
 
   Pack<T, VEC> ra[NV], rw[NV];
@@ -243,13 +210,13 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       if (XF & 1) {
-        // (x - mean) * rstd * gamma + beta, rounded to T as nn.LayerNorm's output;
-        // columns past Kd stay zero
+        // (x - mean) * rstd * gamma + beta as two FMAs (x * rstd + (-mean * rstd)),
+        // rounded to T as nn.LayerNorm's output; columns past Kd stay zero
         const float2 st = *reinterpret_cast<const float2*>(&ln_row[2 * rowv[i]]);
 #pragma unroll
         for (int t = 0; t < VEC; ++t) {
-          float y = (ldf(&ra[i].e[t]) - st.x) * st.y;
-          y = y * gv[t] + bv[t];
+          float y = __builtin_fmaf(ldf(&ra[i].e[t]), st.x, st.y);
+          y = __builtin_fmaf(y, gv[t], bv[t]);
           if (!FAST && k0 + kvv[i] + t >= g.Kd) y = 0.0f;
           stf(&ra[i].e[t], y);
         }
@@ -270,6 +237,42 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
   fetch(0);
+  if (XF & 1) {
+    // (after the first tile's loads are issued, so both latencies overlap)
+    // gamma / beta over the k-tiles (Kd <= LN_MAX_K, a multiple of BK)
+    const T* gp = static_cast<const T*>(g.ln_gamma);
+    const T* bp = static_cast<const T*>(g.ln_beta);
+    const int kpad = (g.Kd + BK - 1) / BK * BK;
+    for (int c = tid; c < kpad; c += 256) {
+      const bool in = c < g.Kd;
+      ln_g[c] = in ? (gp ? ldf(gp + c) : 1.0f) : 0.0f;
+      ln_b[c] = (in && bp) ? ldf(bp + c) : 0.0f;
+    }
+    // mean and 1/sqrt(var + eps) of tile row tid from the row's per-tile
+    // (mean, M2) partials (tile t holds min(ROW_STAT_TILE, Kd - t * ROW_STAT_TILE) columns)
+    if (tid < BM) {
+      const int m = min(m0 + tid, g.M - 1);
+      int64_t sr = m;
+      if (g.arow != nullptr) {
+        const int b = m / g.a_rows, rr = m - b * g.a_rows;
+        sr = (int64_t)b * g.a_src_rows + g.arow[rr];
+      }
+      const float* sp = g.ln_stats + sr * (2 * g.ln_parts);
+      float sm = 0.0f;
+      for (int t = 0; t < g.ln_parts; ++t) sm += (float)min(ROW_STAT_TILE, g.Kd - t * ROW_STAT_TILE) * sp[2 * t];
+      const float mean = sm / (float)g.Kd;
+      float q = 0.0f;
+      for (int t = 0; t < g.ln_parts; ++t) {
+        const float d = sp[2 * t] - mean;
+        q += sp[2 * t + 1] + (float)min(ROW_STAT_TILE, g.Kd - t * ROW_STAT_TILE) * d * d;
+      }
+      const float rstd = 1.0f / sqrtf(q / (float)g.Kd + g.ln_eps);
+      ln_row[2 * tid] = rstd;
+      ln_row[2 * tid + 1] = -mean * rstd;
+    }
+    __syncthreads();
+  }
+
   for (int k0 = 0; k0 < g.Kd; k0 += BK) {
     stash(k0);
     __syncthreads();

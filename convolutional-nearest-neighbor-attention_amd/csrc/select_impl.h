@@ -1,5 +1,6 @@
 // Implementation of the fused similarity + streaming top-k kernel; included by
-// select_bf16.hip and select_f32.hip so the two dtypes compile in parallel.
+// select_{bf16,f32}{,_euc}.hip so that the dtypes and the euclidean instances
+// compile in parallel.
 //
 // Replaces layers.py:323-340 followed by torch.topk in layers.py:344, 363,
 // 391, 410 and the sampled self mask layers.py:291-292, 304-305.  The N x Nq
@@ -571,25 +572,19 @@ void select_kernel(SelArgs a) {
   if (SMP && a.cols != nullptr) emit([&](int r) { return (uint32_t)cl[r]; }, reinterpret_cast<uint32_t*>(a.cols));
 }
 
-template <typename T, int NCH, bool EXACT, int KMAX, bool EX = false>
-int launch_k(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
+template <typename T, int NCH, bool EXACT, int KMAX, bool EUC, bool EX = false>
+int launch_k(int sampled, const SelArgs& a, hipStream_t s) {
   auto smem = [&](int qc) {
     return 2 * TJ * (a.dkp + SelCfg<T>::VEC) * sizeof(T) + 2 * TJ * (sizeof(float) + sizeof(int)) + 8 * sizeof(int) +
            (size_t)qc * NT * 6 + (size_t)KMAX * TPB * sizeof(uint64_t);
   };
   const dim3 grid(a.BH * a.rb_per_bh);
-  if (!euclid && !sampled)
-    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, false, false, EX>), grid, dim3(NT),
-                       smem(queue_cap<T, NCH, EXACT, KMAX, false, false>()), s, a);
-  else if (!euclid && sampled)
-    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, false, true, EX>), grid, dim3(NT),
-                       smem(queue_cap<T, NCH, EXACT, KMAX, false, true>()), s, a);
-  else if (euclid && !sampled)
-    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, true, false, EX>), grid, dim3(NT),
-                       smem(queue_cap<T, NCH, EXACT, KMAX, true, false>()), s, a);
+  if (!sampled)
+    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, EUC, false, EX>), grid, dim3(NT),
+                       smem(queue_cap<T, NCH, EXACT, KMAX, EUC, false>()), s, a);
   else
-    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, true, true, EX>), grid, dim3(NT),
-                       smem(queue_cap<T, NCH, EXACT, KMAX, true, true>()), s, a);
+    hipLaunchKernelGGL((select_kernel<T, NCH, EXACT, KMAX, EUC, true, EX>), grid, dim3(NT),
+                       smem(queue_cap<T, NCH, EXACT, KMAX, EUC, true>()), s, a);
   return (int)hipGetLastError();
 }
 
@@ -614,35 +609,35 @@ __global__ __launch_bounds__(256) void sel_weights_kernel(const float* vals, flo
 }
 
 // one list of KMAX entries, or rounds of 32 for wider selections
-template <typename T, int NCH, bool EXACT>
-int launch_rounds(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
-  if (EXACT && a.Ksel <= 9) return launch_k<T, NCH, EXACT, 9>(euclid, sampled, a, s);
-  if (EXACT && a.Ksel <= 16) return launch_k<T, NCH, EXACT, 16>(euclid, sampled, a, s);
-  if (a.Ksel <= 32) return launch_k<T, NCH, EXACT, 32>(euclid, sampled, a, s);
+template <typename T, int NCH, bool EXACT, bool EUC>
+int launch_rounds(int sampled, const SelArgs& a, hipStream_t s) {
+  if (EXACT && a.Ksel <= 9) return launch_k<T, NCH, EXACT, 9, EUC>(sampled, a, s);
+  if (EXACT && a.Ksel <= 16) return launch_k<T, NCH, EXACT, 16, EUC>(sampled, a, s);
+  if (a.Ksel <= 32) return launch_k<T, NCH, EXACT, 32, EUC>(sampled, a, s);
   SelArgs r = a;
   r.w = nullptr;
   for (int base = 0; base < a.Ksel; base += 32) {
     r.kbase = base;
     r.Ksel = min(32, a.Ksel - base);
-    const int st = base == 0 ? launch_k<T, NCH, EXACT, 32, false>(euclid, sampled, r, s)
-                             : launch_k<T, NCH, EXACT, 32, true>(euclid, sampled, r, s);
+    const int st = base == 0 ? launch_k<T, NCH, EXACT, 32, EUC, false>(sampled, r, s)
+                             : launch_k<T, NCH, EXACT, 32, EUC, true>(sampled, r, s);
     if (st) return st;
   }
   if (a.w != nullptr) {
     const int64_t rows = (int64_t)a.BH * a.N;
     hipLaunchKernelGGL(sel_weights_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, a.vals, a.w,
-                       rows, a.K, a.softmax, euclid);
+                       rows, a.K, a.softmax, (int)EUC);
   }
   return (int)hipGetLastError();
 }
 
-template <typename T, int NCH>
-int launch_n(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
-  return launch_rounds<T, NCH, true>(euclid, sampled, a, s);
+template <typename T, int NCH, bool EUC>
+int launch_n(int sampled, const SelArgs& a, hipStream_t s) {
+  return launch_rounds<T, NCH, true, EUC>(sampled, a, s);
 }
 
-template <typename T>
-int launch_select_t(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
+template <typename T, bool EUC>
+int launch_select_t(int sampled, const SelArgs& a, hipStream_t s) {
   if (a.dkp % Mfma<T>::KC != 0 || a.dkp > SelCfg<T>::MAXCH * Mfma<T>::KC || a.dkp % SelCfg<T>::VEC != 0)
     return CNNA_ERR_SHAPE;
   if (a.Nq > 65536) return CNNA_ERR_SHAPE;
@@ -650,12 +645,12 @@ int launch_select_t(int euclid, int sampled, const SelArgs& a, hipStream_t s) {
   static_assert(TPB * 32 * 2 <= QCMIN * NT * 3, "output staging must fit the queue region");
   const int nch = a.dkp / Mfma<T>::KC;
   constexpr int q = SelCfg<T>::MAXCH / 4;   // head widths 32, 64, 128, 256 (bf16) / 16 .. 128 (f32)
-  if (nch == q / 2) return launch_n<T, q / 2>(euclid, sampled, a, s);
-  if (nch == q) return launch_n<T, q>(euclid, sampled, a, s);
-  if (nch == 2 * q) return launch_n<T, 2 * q>(euclid, sampled, a, s);
-  if (nch == 4 * q) return launch_n<T, 4 * q>(euclid, sampled, a, s);
+  if (nch == q / 2) return launch_n<T, q / 2, EUC>(sampled, a, s);
+  if (nch == q) return launch_n<T, q, EUC>(sampled, a, s);
+  if (nch == 2 * q) return launch_n<T, 2 * q, EUC>(sampled, a, s);
+  if (nch == 4 * q) return launch_n<T, 4 * q, EUC>(sampled, a, s);
   // other widths: guarded chunks, lists of 32
-  return launch_rounds<T, SelCfg<T>::MAXCH, false>(euclid, sampled, a, s);
+  return launch_rounds<T, SelCfg<T>::MAXCH, false, EUC>(sampled, a, s);
 }
 
 }  // namespace
