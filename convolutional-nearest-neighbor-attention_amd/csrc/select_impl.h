@@ -26,7 +26,8 @@
 //
 // Two passes over the candidates:
 //  1. per lane, the maximum of each 16-candidate group (4-candidate groups
-//     when Nq <= 512) goes into a sorted
+//     when Nq <= 512; for d >= 256 on rows of at least 64 tiles only the
+//     first quarter of the tiles is swept) goes into a sorted
 //     register list (med3 insertion); the K-th largest of the union of both
 //     half-lanes' lists is a lower bound tau of the token's K-th key, because
 //     it is attained by K distinct candidates.
@@ -304,8 +305,9 @@ void select_kernel(SelArgs a) {
   // VALU work on tile t, so the matrix and vector pipes overlap within a wave.
   // Tile t lives in LDS buffer t&1; tile t+2 is staged into that buffer once
   // every wave is done with tile t, and tile t+3 is fetched into registers.
-  // process(acc, buf, j0) consumes one tile's accumulators.
-  auto sweep = [&](auto&& process) __attribute__((always_inline)) {
+  // process(acc, buf, j0) consumes one tile's accumulators; the sweep covers
+  // the first ntiles tiles.
+  auto sweep = [&](auto&& process, const int ntiles) __attribute__((always_inline)) {
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, PD - 1>;
     f32x16_t accA[NB], accB[NB];
@@ -358,6 +360,12 @@ void select_kernel(SelArgs a) {
     // tau is the exact K-th key and only about K candidates reach the queues.
     const bool every = KMAX >= 16 && ntiles <= 8;
     const bool fine = ntiles <= 16;
+    // Wide heads on long rows (d >= 256, at least 64 tiles: config 5) draw the
+    // bound from the first quarter of the tiles: any candidates give a valid
+    // bound, and there one sweep costs more than the extra passers it lets
+    // through (c5 select 598 -> 521 us; at d = 128 the extra passers cost more
+    // than the sweep saves, and the whole row is used).
+    const int p1 = (NCH * Mfma<T>::KC >= 256 && ntiles >= 64) ? (ntiles + 3) / 4 : ntiles;
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) L[r] = -INFINITY;
     // MASKED: the tile runs past Nq (only the last one); its extra rows drop out
@@ -394,7 +402,7 @@ void select_kernel(SelArgs a) {
         bound_tile(acc, buf, j0, std::false_type{});
       else
         bound_tile(acc, buf, j0, std::true_type{});
-    });
+    }, p1);
     {
       float P[KMAX];
 #pragma unroll
@@ -481,7 +489,7 @@ void select_kernel(SelArgs a) {
         filter_tile(acc, buf, j0, std::false_type{});
       else
         filter_tile(acc, buf, j0, std::true_type{});
-    });
+    }, ntiles);
     drain();
   }
 
