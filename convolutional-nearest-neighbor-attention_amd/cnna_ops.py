@@ -18,7 +18,7 @@ from torch.utils._python_dispatch import _get_current_dispatch_mode
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libcnna.so")
 
-CNNA_F32, CNNA_BF16 = 0, 1
+CNNA_F32, CNNA_BF16, CNNA_F16 = 0, 1, 2
 METRICS = {"matmul": 0, "cosine": 1, "euclidean": 2}
 CONVS = {"standard": 0, "depthwise": 1, "depthwise-separable": 2}
 MERGE_REFERENCE, MERGE_CONCAT = 0, 1
@@ -145,7 +145,9 @@ def dtype_code(dt: torch.dtype) -> int:
         return CNNA_F32
     if dt == torch.bfloat16:
         return CNNA_BF16
-    raise TypeError(f"cnna: unsupported dtype {dt} (float32 or bfloat16)")
+    if dt == torch.float16:
+        return CNNA_F16
+    raise TypeError(f"cnna: unsupported dtype {dt} (float32, bfloat16 or float16)")
 
 
 def make_desc(B, N, C, H, Nq, K, seq_length, dtype, metric, conv, softmax, sampled, coord,
@@ -308,7 +310,7 @@ def linear(a, W, bias=None, gelu=False, residual=None, ln=None, want_stats=False
     ``ln``: a :class:`FoldedNorm` of a's rows; the GEMM then runs on
     LayerNorm(a), normalised as it loads a.  ``want_stats``: also return the
     row-statistics partials of the output (a :class:`FoldedNorm` without its
-    module), from the GEMM's epilogue where the library supports it (bf16,
+    module), from the GEMM's epilogue where the library supports it (16-bit,
     aligned rows), else from a statistics pass over the output."""
     ar = _rows(a)
     M, Kd = ar.shape
@@ -338,9 +340,10 @@ def stat_parts(C: int) -> int:
 
 
 def _stats_epilogue_ok(out: torch.Tensor, rr: Optional[torch.Tensor]) -> bool:
-    """The GEMM's statistics epilogue applies (bf16, Nout % 8 == 0, 16-byte
-    aligned rows); otherwise the statistics come from ``row_stats``."""
-    if out.dtype != torch.bfloat16 or out.shape[1] % 8 or out.data_ptr() % 16 or out.stride(0) % 8:
+    """The GEMM's statistics epilogue applies (bf16 / fp16, Nout % 8 == 0,
+    16-byte aligned rows); otherwise the statistics come from ``row_stats``."""
+    if (out.dtype not in (torch.bfloat16, torch.float16) or out.shape[1] % 8 or out.data_ptr() % 16
+            or out.stride(0) % 8):
         return False
     return rr is None or (rr.data_ptr() % 16 == 0 and rr.stride(0) % 8 == 0)
 

@@ -28,33 +28,36 @@ __host__ __device__ inline bool merge_mixes(const AggArgs& a) {
 }
 
 template <typename T, int VW> struct Vec;
-template <> struct Vec<uint16_t, 8> {
+// eight 16-bit values (bf16 or fp16) as one 16-byte vector
+template <typename T> struct Vec16 {
   typedef uint4 Raw;
-  static CNNA_DEV Raw raw(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
-  static CNNA_DEV void load(const uint16_t* p, float (&o)[8]) { unpack(raw(p), o); }
+  static CNNA_DEV Raw raw(const T* p) { return *reinterpret_cast<const uint4*>(p); }
+  static CNNA_DEV void load(const T* p, float (&o)[8]) { unpack(raw(p), o); }
   static CNNA_DEV void unpack(const uint4 u, float (&o)[8]) {
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      o[2 * i] = __uint_as_float(w[i] << 16);
-      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      o[2 * i] = Pair16<T>::lo(w[i]);
+      o[2 * i + 1] = Pair16<T>::hi(w[i]);
     }
   }
-  static CNNA_DEV void store(uint16_t* p, const float (&o)[8]) {
+  static CNNA_DEV void store(T* p, const float (&o)[8]) {
     u32x4_t w;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = f2bf2(o[2 * i], o[2 * i + 1]);
+    for (int i = 0; i < 4; ++i) w[i] = Pair16<T>::pack(o[2 * i], o[2 * i + 1]);
     *reinterpret_cast<u32x4_t*>(p) = w;
   }
   static CNNA_DEV Raw pack(const float (&o)[8]) {
     Raw u;
-    u.x = f2bf2(o[0], o[1]);
-    u.y = f2bf2(o[2], o[3]);
-    u.z = f2bf2(o[4], o[5]);
-    u.w = f2bf2(o[6], o[7]);
+    u.x = Pair16<T>::pack(o[0], o[1]);
+    u.y = Pair16<T>::pack(o[2], o[3]);
+    u.z = Pair16<T>::pack(o[4], o[5]);
+    u.w = Pair16<T>::pack(o[6], o[7]);
     return u;
   }
 };
+template <> struct Vec<uint16_t, 8> : Vec16<uint16_t> {};
+template <> struct Vec<_Float16, 8> : Vec16<_Float16> {};
 template <> struct Vec<float, 4> {
   typedef float4 Raw;
   static CNNA_DEV Raw raw(const float* p) { return *reinterpret_cast<const float4*>(p); }
@@ -333,6 +336,7 @@ int launch_vw(const AggArgs& a0, hipStream_t s) {
 int launch_aggregate(int dtype, const AggArgs& a, hipStream_t s) {
   if (a.BH <= 0 || a.N <= 0) return 0;
   if (dtype == CNNA_BF16) return launch_vw<uint16_t, false>(a, s);
+  if (dtype == CNNA_F16) return launch_vw<_Float16, false>(a, s);
   if (dtype == CNNA_F32) return launch_vw<float, false>(a, s);
   return CNNA_ERR_DTYPE;
 }
@@ -340,6 +344,7 @@ int launch_aggregate(int dtype, const AggArgs& a, hipStream_t s) {
 int launch_merge(int dtype, const AggArgs& a, hipStream_t s) {
   if (a.BH <= 0 || a.N <= 0) return 0;
   if (dtype == CNNA_BF16) return launch_vw<uint16_t, true>(a, s);
+  if (dtype == CNNA_F16) return launch_vw<_Float16, true>(a, s);
   if (dtype == CNNA_F32) return launch_vw<float, true>(a, s);
   return CNNA_ERR_DTYPE;
 }

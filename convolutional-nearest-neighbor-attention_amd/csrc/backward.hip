@@ -31,36 +31,45 @@ CNNA_DEV float wave_sum(float x) {
 
 // CPL consecutive channels starting at c0 of a row; zero beyond lim.
 template <typename T, int CPL> struct Row;
-template <> struct Row<uint16_t, 1> {
-  static CNNA_DEV void load(const uint16_t* p, float (&o)[1]) { o[0] = bf2f(*p); }
+// 16-bit rows (bf16 or fp16)
+template <typename T> struct Row16_1 {
+  static CNNA_DEV void load(const T* p, float (&o)[1]) { o[0] = ldf(p); }
 };
-template <> struct Row<uint16_t, 2> {
-  static CNNA_DEV void load(const uint16_t* p, float (&o)[2]) {
+template <typename T> struct Row16_2 {
+  static CNNA_DEV void load(const T* p, float (&o)[2]) {
     const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
-    o[0] = __uint_as_float(u << 16);
-    o[1] = __uint_as_float(u & 0xffff0000u);
+    o[0] = Pair16<T>::lo(u);
+    o[1] = Pair16<T>::hi(u);
   }
 };
-template <> struct Row<uint16_t, 4> {
-  static CNNA_DEV void load(const uint16_t* p, float (&o)[4]) {
+template <typename T> struct Row16_4 {
+  static CNNA_DEV void load(const T* p, float (&o)[4]) {
     const uint2 u = *reinterpret_cast<const uint2*>(p);
-    o[0] = __uint_as_float(u.x << 16);
-    o[1] = __uint_as_float(u.x & 0xffff0000u);
-    o[2] = __uint_as_float(u.y << 16);
-    o[3] = __uint_as_float(u.y & 0xffff0000u);
+    o[0] = Pair16<T>::lo(u.x);
+    o[1] = Pair16<T>::hi(u.x);
+    o[2] = Pair16<T>::lo(u.y);
+    o[3] = Pair16<T>::hi(u.y);
   }
 };
-template <> struct Row<uint16_t, 8> {
-  static CNNA_DEV void load(const uint16_t* p, float (&o)[8]) {
+template <typename T> struct Row16_8 {
+  static CNNA_DEV void load(const T* p, float (&o)[8]) {
     const uint4 u = *reinterpret_cast<const uint4*>(p);
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      o[2 * i] = __uint_as_float(w[i] << 16);
-      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      o[2 * i] = Pair16<T>::lo(w[i]);
+      o[2 * i + 1] = Pair16<T>::hi(w[i]);
     }
   }
 };
+template <> struct Row<uint16_t, 1> : Row16_1<uint16_t> {};
+template <> struct Row<uint16_t, 2> : Row16_2<uint16_t> {};
+template <> struct Row<uint16_t, 4> : Row16_4<uint16_t> {};
+template <> struct Row<uint16_t, 8> : Row16_8<uint16_t> {};
+template <> struct Row<_Float16, 1> : Row16_1<_Float16> {};
+template <> struct Row<_Float16, 2> : Row16_2<_Float16> {};
+template <> struct Row<_Float16, 4> : Row16_4<_Float16> {};
+template <> struct Row<_Float16, 8> : Row16_8<_Float16> {};
 template <> struct Row<float, 1> {
   static CNNA_DEV void load(const float* p, float (&o)[1]) { o[0] = *p; }
 };
@@ -946,6 +955,9 @@ int launch_unmerge(int dtype, const void* dz, void* dy, int BH, int N, int dk, i
     if (dtype == CNNA_BF16)
       hipLaunchKernelGGL(unmerge_tile_kernel<uint16_t>, grid, dim3(256), 0, s,
                          static_cast<const uint16_t*>(dz), static_cast<uint16_t*>(dy), N, dk, H, C);
+    else if (dtype == CNNA_F16)
+      hipLaunchKernelGGL(unmerge_tile_kernel<_Float16>, grid, dim3(256), 0, s,
+                         static_cast<const _Float16*>(dz), static_cast<_Float16*>(dy), N, dk, H, C);
     else if (dtype == CNNA_F32)
       hipLaunchKernelGGL(unmerge_tile_kernel<float>, grid, dim3(256), 0, s,
                          static_cast<const float*>(dz), static_cast<float*>(dy), N, dk, H, C);
@@ -956,6 +968,9 @@ int launch_unmerge(int dtype, const void* dz, void* dy, int BH, int N, int dk, i
   if (dtype == CNNA_BF16)
     hipLaunchKernelGGL(unmerge_kernel<uint16_t>, grid_for(n), dim3(256), 0, s,
                        static_cast<const uint16_t*>(dz), static_cast<uint16_t*>(dy), BH, N, dk, H, C, concat);
+  else if (dtype == CNNA_F16)
+    hipLaunchKernelGGL(unmerge_kernel<_Float16>, grid_for(n), dim3(256), 0, s,
+                       static_cast<const _Float16*>(dz), static_cast<_Float16*>(dy), BH, N, dk, H, C, concat);
   else if (dtype == CNNA_F32)
     hipLaunchKernelGGL(unmerge_kernel<float>, grid_for(n), dim3(256), 0, s,
                        static_cast<const float*>(dz), static_cast<float*>(dy), BH, N, dk, H, C, concat);
@@ -969,6 +984,7 @@ int launch_tok_bwd(int dtype, const TokBwdArgs& a0, hipStream_t s) {
   TokBwdArgs a = a0;
   a.nblk = tok_bwd_blocks(a.BH, a.N);
   if (dtype == CNNA_BF16) return launch_tok_c<uint16_t>(a, s);
+  else if (dtype == CNNA_F16) return launch_tok_c<_Float16>(a, s);
   if (dtype == CNNA_F32) return launch_tok_c<float>(a, s);
   return CNNA_ERR_DTYPE;
 }
@@ -979,6 +995,9 @@ int launch_w0_reduce(int dtype, const float* part, int nblk, int n, void* out, h
   if (dtype == CNNA_BF16)
     hipLaunchKernelGGL(w0_reduce_kernel<uint16_t>, grid, dim3(1024), 0, s, part, nblk, n,
                        static_cast<uint16_t*>(out));
+  else if (dtype == CNNA_F16)
+    hipLaunchKernelGGL(w0_reduce_kernel<_Float16>, grid, dim3(1024), 0, s, part, nblk, n,
+                       static_cast<_Float16*>(out));
   else if (dtype == CNNA_F32)
     hipLaunchKernelGGL(w0_reduce_kernel<float>, grid, dim3(1024), 0, s, part, nblk, n,
                        static_cast<float*>(out));
@@ -1015,6 +1034,7 @@ int launch_csr(const CsrArgs& c, hipStream_t s) {
 
 int launch_pull(int dtype, const PullArgs& p, hipStream_t s) {
   if (dtype == CNNA_BF16) return launch_pull_t<uint16_t>(p, s);
+  else if (dtype == CNNA_F16) return launch_pull_t<_Float16>(p, s);
   if (dtype == CNNA_F32) return launch_pull_t<float>(p, s);
   return CNNA_ERR_DTYPE;
 }
@@ -1026,6 +1046,10 @@ int launch_gather_rows(int dtype, const void* x, int64_t ldx, const int32_t* can
   if (dtype == CNNA_BF16)
     hipLaunchKernelGGL(gather_rows_kernel<uint16_t>, grid_for(n), dim3(256), 0, s,
                        static_cast<const uint16_t*>(x), ldx, cand, static_cast<uint16_t*>(xs), B, N,
+                       Nq, C);
+  else if (dtype == CNNA_F16)
+    hipLaunchKernelGGL(gather_rows_kernel<_Float16>, grid_for(n), dim3(256), 0, s,
+                       static_cast<const _Float16*>(x), ldx, cand, static_cast<_Float16*>(xs), B, N,
                        Nq, C);
   else if (dtype == CNNA_F32)
     hipLaunchKernelGGL(gather_rows_kernel<float>, grid_for(n), dim3(256), 0, s,
@@ -1042,6 +1066,10 @@ int launch_scatter_rows(int dtype, const void* dxs, const int32_t* cand, void* d
   if (dtype == CNNA_BF16)
     hipLaunchKernelGGL(scatter_rows_kernel<uint16_t>, grid_for(n), dim3(256), 0, s,
                        static_cast<const uint16_t*>(dxs), cand, static_cast<uint16_t*>(dx), B, N, Nq,
+                       C);
+  else if (dtype == CNNA_F16)
+    hipLaunchKernelGGL(scatter_rows_kernel<_Float16>, grid_for(n), dim3(256), 0, s,
+                       static_cast<const _Float16*>(dxs), cand, static_cast<_Float16*>(dx), B, N, Nq,
                        C);
   else if (dtype == CNNA_F32)
     hipLaunchKernelGGL(scatter_rows_kernel<float>, grid_for(n), dim3(256), 0, s,

@@ -14,8 +14,6 @@
 
 namespace {
 
-CNNA_DEV float rnd(float v, uint16_t) { return bf2f(f2bf(v)); }
-CNNA_DEV float rnd(float v, float) { return v; }
 
 CNNA_DEV float wave_sum(float v) {
 #pragma unroll
@@ -38,7 +36,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(LnArgs a) {
     v[e] = 0.0f;
     if (c < a.C) {
       float t = ldf(x + c);
-      if (r != nullptr) t = rnd(t + ldf(r + c), T(0));
+      if (r != nullptr) t = rnd_to(t + ldf(r + c), T(0));
       v[e] = t;
       s += t;
     }
@@ -102,7 +100,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(LnArgs a) {
 #pragma unroll
       for (int u = 0; u < VEC; ++u) {
         float t = ldf(&lx.t[u]);
-        if (r != nullptr) t = rnd(t + ldf(&lr.t[u]), T(0));
+        if (r != nullptr) t = rnd_to(t + ldf(&lr.t[u]), T(0));
         v[e][u] = t;
         s += t;
       }
@@ -216,6 +214,8 @@ int launch_layernorm(int dtype, const LnArgs& a, hipStream_t s) {
     const dim3 grid((unsigned)((a.rows + 3) / 4));
     if (dtype == CNNA_BF16)
       hipLaunchKernelGGL(row_stats_kernel<uint16_t>, grid, dim3(256), 0, s, a);
+    else if (dtype == CNNA_F16)
+      hipLaunchKernelGGL(row_stats_kernel<_Float16>, grid, dim3(256), 0, s, a);
     else if (dtype == CNNA_F32)
       hipLaunchKernelGGL(row_stats_kernel<float>, grid, dim3(256), 0, s, a);
     else
@@ -223,6 +223,7 @@ int launch_layernorm(int dtype, const LnArgs& a, hipStream_t s) {
     return (int)hipGetLastError();
   }
   if (dtype == CNNA_BF16) return launch_ln_t<uint16_t>(a, s);
+  else if (dtype == CNNA_F16) return launch_ln_t<_Float16>(a, s);
   if (dtype == CNNA_F32) return launch_ln_t<float>(a, s);
   return CNNA_ERR_DTYPE;
 }

@@ -135,6 +135,7 @@ int launch_conv1d_tokens(int dtype, const Conv1dArgs& a, hipStream_t s) {
   if (a.dk <= 0 || a.ks <= 0 || a.ks > 33 || a.H <= 0 || a.padl < 0 || a.padl >= a.ks)
     return CNNA_ERR_SHAPE;
   if (dtype == CNNA_BF16) return launch_t<uint16_t>(a, s);
+  else if (dtype == CNNA_F16) return launch_t<_Float16>(a, s);
   if (dtype == CNNA_F32) return launch_t<float>(a, s);
   return CNNA_ERR_DTYPE;
 }

@@ -23,7 +23,7 @@ const char* cnna_error_string(int code) {
     case CNNA_OK: return "ok";
     case CNNA_ERR_NULL: return "cnna: required pointer is NULL";
     case CNNA_ERR_SHAPE: return "cnna: inconsistent or unsupported shape";
-    case CNNA_ERR_DTYPE: return "cnna: unsupported dtype (float32 or bfloat16)";
+    case CNNA_ERR_DTYPE: return "cnna: unsupported dtype (float32, bfloat16 or float16)";
     case CNNA_ERR_OPTION: return "cnna: unknown magnitude_type / convolution_type / option combination";
     case CNNA_ERR_K_RANGE: return "cnna: selected index k out of range";
     case CNNA_ERR_SEQ_LENGTH: return "cnna: seq_length must equal the number of tokens when num_heads > 1";
@@ -34,7 +34,7 @@ const char* cnna_error_string(int code) {
              "cnna_forward_noalloc; call cnna_forward with a workspace";
     case CNNA_ERR_UNSUPPORTED:
       return "cnna: configuration not supported by this build (limits: K <= 64 neighbours in the "
-             "backward, head width d_k (+1 with coordinate encoding) <= 256 for bfloat16 and <= 128 for "
+             "backward, head width d_k (+1 with coordinate encoding) <= 256 for 16-bit types and <= 128 for "
              "float32, at most 65536 candidates; folded LayerNorm: C <= 1024; row statistics "
              "epilogue: bfloat16, Nout % 8 == 0, 16-byte aligned out / res with row strides that "
              "are multiples of 8 elements)";
@@ -46,7 +46,7 @@ const char* cnna_error_string(int code) {
 
 int cnna_check_desc(const cnna_desc* d) {
   if (d == nullptr) return CNNA_ERR_NULL;
-  if (d->dtype != CNNA_F32 && d->dtype != CNNA_BF16) return CNNA_ERR_DTYPE;
+  if (d->dtype != CNNA_F32 && d->dtype != CNNA_BF16 && d->dtype != CNNA_F16) return CNNA_ERR_DTYPE;
   if (d->B <= 0 || d->N <= 0 || d->C <= 0 || d->H <= 0 || d->C % d->H != 0) return CNNA_ERR_SHAPE;
   if (d->metric < CNNA_MATMUL || d->metric > CNNA_EUCLIDEAN) return CNNA_ERR_OPTION;
   if (d->conv < CNNA_CONV_STANDARD || d->conv > CNNA_CONV_DWSEP) return CNNA_ERR_OPTION;
@@ -59,7 +59,7 @@ int cnna_check_desc(const cnna_desc* d) {
   if (d->merge == CNNA_MERGE_REFERENCE && d->H > 1 && d->seq_length != d->N) return CNNA_ERR_SEQ_LENGTH;
   // the reference accepts these; the kernels' tiles do not
   const int dkp = dkp_of(d);
-  if (d->dtype == CNNA_BF16 && dkp > 256) return CNNA_ERR_UNSUPPORTED;
+  if (d->dtype != CNNA_F32 && dkp > 256) return CNNA_ERR_UNSUPPORTED;
   if (d->dtype == CNNA_F32 && dkp > 128) return CNNA_ERR_UNSUPPORTED;
   if (d->Nq > 65536) return CNNA_ERR_UNSUPPORTED;
   return CNNA_OK;
@@ -303,7 +303,7 @@ int cnna_output_proj(const cnna_desc* d, const void* z, const void* Wo, void* ou
 int cnna_layernorm(int32_t dtype, int64_t rows, int32_t C, const void* x, int64_t ldx, const void* res,
                    int64_t ldr, void* sum_out, int64_t ld_sum, const void* gamma, const void* beta,
                    float eps, void* y, int64_t ldy, void* stream) {
-  if (dtype != CNNA_F32 && dtype != CNNA_BF16) return CNNA_ERR_DTYPE;
+  if (dtype != CNNA_F32 && dtype != CNNA_BF16 && dtype != CNNA_F16) return CNNA_ERR_DTYPE;
   if (rows < 0 || C <= 0 || C > 1024 || ldx < C || ldy < C || (res && ldr < C) || (sum_out && ld_sum < C))
     return CNNA_ERR_SHAPE;
   if (rows > 0 && (!x || !y)) return CNNA_ERR_NULL;
@@ -327,7 +327,7 @@ int cnna_layernorm(int32_t dtype, int64_t rows, int32_t C, const void* x, int64_
 
 int cnna_row_stats(int32_t dtype, int64_t rows, int32_t C, const void* x, int64_t ldx, float* stats,
                    void* stream) {
-  if (dtype != CNNA_F32 && dtype != CNNA_BF16) return CNNA_ERR_DTYPE;
+  if (dtype != CNNA_F32 && dtype != CNNA_BF16 && dtype != CNNA_F16) return CNNA_ERR_DTYPE;
   if (rows < 0 || C <= 0 || ldx < C) return CNNA_ERR_SHAPE;
   if (rows == 0) return 0;
   if (!x || !stats) return CNNA_ERR_NULL;
@@ -352,7 +352,7 @@ int cnna_linear(int32_t dtype, int64_t M, int32_t Nout, int32_t Kd, const void* 
 int cnna_linear_ln(int32_t dtype, int64_t M, int32_t Nout, int32_t Kd, const void* a, int64_t lda,
                    const cnna_ln* ln, const void* W, const void* bias, int32_t act, const void* res,
                    int64_t ldr, void* out, int64_t ldo, float* stats_out, void* stream) {
-  if (dtype != CNNA_F32 && dtype != CNNA_BF16) return CNNA_ERR_DTYPE;
+  if (dtype != CNNA_F32 && dtype != CNNA_BF16 && dtype != CNNA_F16) return CNNA_ERR_DTYPE;
   if (act != CNNA_ACT_NONE && act != CNNA_ACT_GELU) return CNNA_ERR_OPTION;
   if (M < 0 || M > INT32_MAX || Nout <= 0 || Kd <= 0 || lda < Kd || ldo < Nout || (res && ldr < Nout))
     return CNNA_ERR_SHAPE;

@@ -1,8 +1,9 @@
 // Shared device helpers for the ConvNN-Attention HIP library (gfx950 only).
 //
 // Storage types: float for fp32 tensors, uint16_t holding the bf16 bit
-// pattern for bf16 tensors.  All arithmetic is fp32; bf16 is rounded to
-// nearest-even when stored, the same rounding torch applies.
+// pattern for bf16 tensors, _Float16 for fp16 tensors.  All arithmetic is
+// fp32; 16-bit values are rounded to nearest-even when stored, the same
+// rounding torch applies.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -33,8 +34,34 @@ CNNA_DEV uint32_t f2bf2(float lo, float hi) {
 
 CNNA_DEV float ldf(const float* p) { return *p; }
 CNNA_DEV float ldf(const uint16_t* p) { return bf2f(*p); }
+CNNA_DEV float ldf(const _Float16* p) { return (float)*p; }
 CNNA_DEV void stf(float* p, float v) { *p = v; }
 CNNA_DEV void stf(uint16_t* p, float v) { *p = f2bf(v); }
+CNNA_DEV void stf(_Float16* p, float v) { *p = (_Float16)v; }
+
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+// Pairs of 16-bit values packed in a 32-bit word (element 0 in the low half),
+// for either 16-bit storage type.
+template <typename T> struct Pair16;
+template <> struct Pair16<uint16_t> {
+  static CNNA_DEV float lo(uint32_t u) { return __uint_as_float(u << 16); }
+  static CNNA_DEV float hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+  static CNNA_DEV uint32_t pack(float lo, float hi) { return f2bf2(lo, hi); }
+};
+template <> struct Pair16<_Float16> {
+  static CNNA_DEV float lo(uint32_t u) { return (float)__builtin_bit_cast(f16x2_t, u)[0]; }
+  static CNNA_DEV float hi(uint32_t u) { return (float)__builtin_bit_cast(f16x2_t, u)[1]; }
+  static CNNA_DEV uint32_t pack(float lo, float hi) {
+    const f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
+  }
+};
+// v rounded to the storage type T and back (what storing a T and reading it gives)
+CNNA_DEV float rnd_to(float v, float) { return v; }
+CNNA_DEV float rnd_to(float v, uint16_t) { return bf2f(f2bf(v)); }
+CNNA_DEV float rnd_to(float v, _Float16) { return (float)(_Float16)v; }
 
 // Smallest float strictly greater than x (x not NaN).
 CNNA_DEV float next_up(float x) {
@@ -45,7 +72,7 @@ CNNA_DEV float next_up(float x) {
   return __uint_as_float(u);
 }
 
-// MFMA 32x32 traits.  Operand layout of v_mfma_f32_32x32x{16_bf16,2_f32}:
+// MFMA 32x32 traits.  Operand layout of v_mfma_f32_32x32x{16_bf16,16_f16,2_f32}:
 //   A (32 x KC): lane l supplies A[l % 32][(l / 32) * KL + 0..KL-1]
 //   B (KC x 32): lane l supplies B[(l / 32) * KL + 0..KL-1][l % 32]
 //   D (32 x 32): lane l, register v holds D[(v/4)*8 + (l/32)*4 + v%4][l % 32]
@@ -68,6 +95,25 @@ template <> struct Mfma<uint16_t> {
   }
   static CNNA_DEV f32x16_t mma(frag a, frag b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma<_Float16> {
+  static constexpr int KC = 16;
+  static constexpr int KL = 8;
+  typedef f16x8_t frag;
+  static CNNA_DEV frag load(const _Float16* p) {
+    uint4 u = *reinterpret_cast<const uint4*>(p);
+    return __builtin_bit_cast(frag, u);
+  }
+  static CNNA_DEV frag zero() { return __builtin_bit_cast(frag, make_uint4(0, 0, 0, 0)); }
+  static CNNA_DEV frag neg(frag a) {
+    u32x4_t u = __builtin_bit_cast(u32x4_t, a);
+    u ^= 0x80008000u;
+    return __builtin_bit_cast(frag, u);
+  }
+  static CNNA_DEV f32x16_t mma(frag a, frag b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
 };
 

@@ -9,7 +9,9 @@
 
 namespace cnna_desc_util {
 
-inline int elem_size(int dtype) { return dtype == CNNA_BF16 ? 2 : (dtype == CNNA_F32 ? 4 : 0); }
+inline int elem_size(int dtype) {
+  return (dtype == CNNA_BF16 || dtype == CNNA_F16) ? 2 : (dtype == CNNA_F32 ? 4 : 0);
+}
 
 inline int din_of(const cnna_desc* d) { return d->C / d->H + (d->coord ? 1 : 0); }
 

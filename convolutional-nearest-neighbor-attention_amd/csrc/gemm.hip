@@ -33,6 +33,7 @@ constexpr int LN_MAX_K = 1024;
 
 template <typename T> struct GemmCfg;
 template <> struct GemmCfg<uint16_t> { static constexpr int BK = 64, VEC = 8; };
+template <> struct GemmCfg<_Float16> { static constexpr int BK = 64, VEC = 8; };
 template <> struct GemmCfg<float> { static constexpr int BK = 32, VEC = 4; };
 
 template <typename T, int VEC>
@@ -42,13 +43,15 @@ union Pack {
 };
 
 // w * (16-byte vector of T), rounded back to T
-CNNA_DEV u32x4_t scale_vec(u32x4_t s, float w, uint16_t) {
+template <typename T>
+CNNA_DEV u32x4_t scale_vec16(u32x4_t s, float w) {
   u32x4_t o;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    o[i] = f2bf2(w * __uint_as_float(s[i] << 16), w * __uint_as_float(s[i] & 0xffff0000u));
+  for (int i = 0; i < 4; ++i) o[i] = Pair16<T>::pack(w * Pair16<T>::lo(s[i]), w * Pair16<T>::hi(s[i]));
   return o;
 }
+CNNA_DEV u32x4_t scale_vec(u32x4_t s, float w, uint16_t) { return scale_vec16<uint16_t>(s, w); }
+CNNA_DEV u32x4_t scale_vec(u32x4_t s, float w, _Float16) { return scale_vec16<_Float16>(s, w); }
 CNNA_DEV u32x4_t scale_vec(u32x4_t s, float w, float) {
   u32x4_t o;
 #pragma unroll
@@ -63,19 +66,22 @@ template <typename T, int EPI>
 CNNA_DEV float lin_epi(const GemmArgs& g, float v, int n) {
   if (g.bias != nullptr) v += ldf(static_cast<const T*>(g.bias) + n);
   if (EPI == 2) {
-    if (sizeof(T) == 2) v = bf2f(f2bf(v));
+    v = rnd_to(v, T(0));
     v = gelu_erf(v);
   }
   return v;
 }
 
 // four consecutive outputs -> one 8-byte (bf16) or 16-byte (fp32) store
-CNNA_DEV void store4(uint16_t* p, float a, float b, float c, float d) {
+template <typename T>
+CNNA_DEV void store4_16(T* p, float a, float b, float c, float d) {
   uint2 u;
-  u.x = f2bf2(a, b);
-  u.y = f2bf2(c, d);
+  u.x = Pair16<T>::pack(a, b);
+  u.y = Pair16<T>::pack(c, d);
   *reinterpret_cast<uint2*>(p) = u;
 }
+CNNA_DEV void store4(uint16_t* p, float a, float b, float c, float d) { store4_16(p, a, b, c, d); }
+CNNA_DEV void store4(_Float16* p, float a, float b, float c, float d) { store4_16(p, a, b, c, d); }
 CNNA_DEV void store4(float* p, float a, float b, float c, float d) {
   *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
 }
@@ -294,7 +300,7 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
     __syncthreads();
   }
 
-  if (sizeof(T) == 2 && g.ostage) {
+  if constexpr (sizeof(T) == 2) if (g.ostage) {
     // ---- bf16 epilogue through LDS: the 128 x 128 tile is staged (reusing the
     // operand buffers) and written back as whole 16-byte row segments
     constexpr int CP = BN + 8;                              // staged row pitch
@@ -314,10 +320,10 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
           if (bp != nullptr) {
             if (n + 4 <= g.Nc && ((uintptr_t)(bp + n) % 8) == 0) {
               const uint2 b2 = *reinterpret_cast<const uint2*>(bp + n);
-              bq[vq][0] = __uint_as_float(b2.x << 16);
-              bq[vq][1] = __uint_as_float(b2.x & 0xffff0000u);
-              bq[vq][2] = __uint_as_float(b2.y << 16);
-              bq[vq][3] = __uint_as_float(b2.y & 0xffff0000u);
+              bq[vq][0] = Pair16<T>::lo(b2.x);
+              bq[vq][1] = Pair16<T>::hi(b2.x);
+              bq[vq][2] = Pair16<T>::lo(b2.y);
+              bq[vq][3] = Pair16<T>::hi(b2.y);
             } else {
 #pragma unroll
               for (int u = 0; u < 4; ++u) bq[vq][u] = ldf(bp + min(n + u, g.Nc - 1));
@@ -337,13 +343,13 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
               float v = e[u] + bq[EPI ? vq : 0][u];
-              if (EPI == 2) v = gelu_erf(bf2f(f2bf(v)));   // rounded as nn.Linear's output
+              if (EPI == 2) v = gelu_erf(rnd_to(v, T(0)));   // rounded as nn.Linear's output
               e[u] = v;
             }
           }
           uint2 u;
-          u.x = f2bf2(e[0], e[1]);
-          u.y = f2bf2(e[2], e[3]);
+          u.x = Pair16<T>::pack(e[0], e[1]);
+          u.y = Pair16<T>::pack(e[2], e[3]);
           *reinterpret_cast<uint2*>(&Cs[ml * CP + nl]) = u;
         }
     }
@@ -391,16 +397,16 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
             const u32x4_t rv = *reinterpret_cast<const u32x4_t*>(static_cast<const T*>(g.res) + (int64_t)m * g.ldr + n);
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-              val[q] = f2bf2(__uint_as_float(val[q] << 16) + __uint_as_float(rv[q] << 16),
-                             __uint_as_float(val[q] & 0xffff0000u) + __uint_as_float(rv[q] & 0xffff0000u));
+              val[q] = Pair16<T>::pack(Pair16<T>::lo(val[q]) + Pair16<T>::lo(rv[q]),
+                                       Pair16<T>::hi(val[q]) + Pair16<T>::hi(rv[q]));
           }
           *reinterpret_cast<u32x4_t*>(obase + (int64_t)m * g.ldo + n) = val;
         }
         float xv[8], sm = 0.0f;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          xv[2 * q] = __uint_as_float(val[q] << 16);
-          xv[2 * q + 1] = __uint_as_float(val[q] & 0xffff0000u);
+          xv[2 * q] = Pair16<T>::lo(val[q]);
+          xv[2 * q + 1] = Pair16<T>::hi(val[q]);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) sm += xv[u];
@@ -425,8 +431,8 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
         const u32x4_t r = *reinterpret_cast<const u32x4_t*>(static_cast<const T*>(g.res) + (int64_t)m * g.ldr + n);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          val[q] = f2bf2(__uint_as_float(val[q] << 16) + __uint_as_float(r[q] << 16),
-                         __uint_as_float(val[q] & 0xffff0000u) + __uint_as_float(r[q] & 0xffff0000u));
+          val[q] = Pair16<T>::pack(Pair16<T>::lo(val[q]) + Pair16<T>::lo(r[q]),
+                                   Pair16<T>::hi(val[q]) + Pair16<T>::hi(r[q]));
       }
       T* dst;
       if (OMODE == GEMM_O_HEADSPLIT)
@@ -501,7 +507,7 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
             const int n = min(nq + u, g.Nc - 1);
             float v = lin_epi<T, EPI>(g, a[vq * 4 + u], n);
             if (g.res != nullptr) {
-              if (sizeof(T) == 2) v = bf2f(f2bf(v));
+              v = rnd_to(v, T(0));
               v += ldf(static_cast<const T*>(g.res) + rrow + n);
             }
             a[vq * 4 + u] = v;
@@ -665,6 +671,9 @@ int launch_transpose(int dtype, const void* src, void* dst, int rows, int cols, 
   if (dtype == CNNA_BF16)
     hipLaunchKernelGGL(transpose_kernel<uint16_t>, grid, dim3(256), 0, s,
                        static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), rows, cols, ldd);
+  else if (dtype == CNNA_F16)
+    hipLaunchKernelGGL(transpose_kernel<_Float16>, grid, dim3(256), 0, s,
+                       static_cast<const _Float16*>(src), static_cast<_Float16*>(dst), rows, cols, ldd);
   else if (dtype == CNNA_F32)
     hipLaunchKernelGGL(transpose_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(src),
                        static_cast<float*>(dst), rows, cols, ldd);
@@ -679,6 +688,9 @@ int launch_permute_w0t(int dtype, const void* w0, void* w0t, int dout, int din, 
   if (dtype == CNNA_BF16)
     hipLaunchKernelGGL(permute_w0t_kernel<uint16_t>, grid, dim3(256), 0, s,
                        static_cast<const uint16_t*>(w0), static_cast<uint16_t*>(w0t), dout, din, K);
+  else if (dtype == CNNA_F16)
+    hipLaunchKernelGGL(permute_w0t_kernel<_Float16>, grid, dim3(256), 0, s,
+                       static_cast<const _Float16*>(w0), static_cast<_Float16*>(w0t), dout, din, K);
   else if (dtype == CNNA_F32)
     hipLaunchKernelGGL(permute_w0t_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(w0),
                        static_cast<float*>(w0t), dout, din, K);
@@ -690,6 +702,7 @@ int launch_permute_w0t(int dtype, const void* w0, void* w0t, int dout, int din, 
 int launch_gemm(int dtype, int amode, int omode, const GemmArgs& g, hipStream_t s) {
   if (g.M <= 0 || g.Nc <= 0 || g.Kd <= 0) return 0;
   if (dtype == CNNA_BF16) return launch_t<uint16_t>(amode, omode, g, s);
+  else if (dtype == CNNA_F16) return launch_t<_Float16>(amode, omode, g, s);
   if (dtype == CNNA_F32) return launch_t<float>(amode, omode, g, s);
   return CNNA_ERR_DTYPE;
 }
@@ -700,6 +713,9 @@ int launch_permute_w0(int dtype, const void* w0, void* w0p, int dout, int din, i
   if (dtype == CNNA_BF16)
     hipLaunchKernelGGL(permute_w0_kernel<uint16_t>, grid, dim3(256), 0, s,
                        static_cast<const uint16_t*>(w0), static_cast<uint16_t*>(w0p), dout, din, K);
+  else if (dtype == CNNA_F16)
+    hipLaunchKernelGGL(permute_w0_kernel<_Float16>, grid, dim3(256), 0, s,
+                       static_cast<const _Float16*>(w0), static_cast<_Float16*>(w0p), dout, din, K);
   else if (dtype == CNNA_F32)
     hipLaunchKernelGGL(permute_w0_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(w0),
                        static_cast<float*>(w0p), dout, din, K);

@@ -165,8 +165,10 @@ struct Operand {
         T* dst = &S[lds_off<T>(rb * RV + j, kb * 4)];
         if constexpr (sizeof(T) == 2) {
           uint2 u;
-          u.x = (uint32_t)reg[0].e[j] | ((uint32_t)reg[1].e[j] << 16);
-          u.y = (uint32_t)reg[2].e[j] | ((uint32_t)reg[3].e[j] << 16);
+          u.x = (uint32_t)__builtin_bit_cast(uint16_t, reg[0].e[j]) |
+                ((uint32_t)__builtin_bit_cast(uint16_t, reg[1].e[j]) << 16);
+          u.y = (uint32_t)__builtin_bit_cast(uint16_t, reg[2].e[j]) |
+                ((uint32_t)__builtin_bit_cast(uint16_t, reg[3].e[j]) << 16);
           *reinterpret_cast<uint2*>(dst) = u;
         } else {
           u32x4_t u;
@@ -276,8 +278,8 @@ __global__ __launch_bounds__(256) void gemm_grad_kernel(GradGemmArgs g) {
             T* dst = static_cast<T*>(g.o) + (int64_t)m * g.ldo + n;
             if constexpr (sizeof(T) == 2) {
               uint2 u;
-              u.x = f2bf2(a4[0], a4[1]);
-              u.y = f2bf2(a4[2], a4[3]);
+              u.x = Pair16<T>::pack(a4[0], a4[1]);
+              u.y = Pair16<T>::pack(a4[2], a4[3]);
               *reinterpret_cast<uint2*>(dst) = u;
             } else {
               *reinterpret_cast<float4*>(dst) = make_float4(a4[0], a4[1], a4[2], a4[3]);
@@ -338,7 +340,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs r) {
 int launch_gemm_grad(int dtype, const GradGemmArgs& g0, hipStream_t s) {
   if (g0.M <= 0 || g0.Nc <= 0) return 0;
   GradGemmArgs g = g0;
-  const int es = dtype == CNNA_BF16 ? 2 : 4;
+  const int es = dtype == CNNA_F32 ? 4 : 2;
   const int bk = grad_gemm_bk(dtype);
   if (g.splits < 1) g.splits = 1;
   // fp32 partials when part is given (any split count), else T into o (one split)
@@ -358,6 +360,7 @@ int launch_gemm_grad(int dtype, const GradGemmArgs& g0, hipStream_t s) {
     g.bvec = bv;
   }
   if (dtype == CNNA_BF16) return launch_grad_t<uint16_t>(g, s);
+  else if (dtype == CNNA_F16) return launch_grad_t<_Float16>(g, s);
   if (dtype == CNNA_F32) return launch_grad_t<float>(g, s);
   return CNNA_ERR_DTYPE;
 }
@@ -368,6 +371,8 @@ int launch_splitk_reduce(int dtype, const ReduceArgs& r, hipStream_t s) {
   dim3 grid((unsigned)((MN + 255) / 256));
   if (dtype == CNNA_BF16)
     hipLaunchKernelGGL(splitk_reduce_kernel<uint16_t>, grid, dim3(256), 0, s, r);
+  else if (dtype == CNNA_F16)
+    hipLaunchKernelGGL(splitk_reduce_kernel<_Float16>, grid, dim3(256), 0, s, r);
   else if (dtype == CNNA_F32)
     hipLaunchKernelGGL(splitk_reduce_kernel<float>, grid, dim3(256), 0, s, r);
   else

@@ -44,6 +44,8 @@ int launch_prep(int dtype, const PrepArgs& p, hipStream_t s) {
   dim3 grid((p.rows_total + 3) / 4);
   if (dtype == CNNA_BF16)
     hipLaunchKernelGGL(prep_kernel<uint16_t>, grid, dim3(256), 0, s, p);
+  else if (dtype == CNNA_F16)
+    hipLaunchKernelGGL(prep_kernel<_Float16>, grid, dim3(256), 0, s, p);
   else if (dtype == CNNA_F32)
     hipLaunchKernelGGL(prep_kernel<float>, grid, dim3(256), 0, s, p);
   else

@@ -1,6 +1,6 @@
 // Implementation of the fused similarity + streaming top-k kernel; included by
-// select_{bf16,f32}{,_euc}.hip so that the dtypes and the euclidean instances
-// compile in parallel.
+// select_{bf16,f16,f32}{,_euc}.hip so that the dtypes and the euclidean
+// instances compile in parallel.
 //
 // Replaces layers.py:323-340 followed by torch.topk in layers.py:344, 363,
 // 391, 410 and the sampled self mask layers.py:291-292, 304-305.  The N x Nq
@@ -63,6 +63,7 @@ constexpr int NT = 256;     // threads per block
 
 template <typename T> struct SelCfg;
 template <> struct SelCfg<uint16_t> { static constexpr int MAXCH = 16, VEC = 8; };  // d <= 256
+template <> struct SelCfg<_Float16> { static constexpr int MAXCH = 16, VEC = 8; };  // d <= 256
 template <> struct SelCfg<float> { static constexpr int MAXCH = 64, VEC = 4; };     // d <= 128
 
 // A (key, index) pair as one 64-bit integer ordered like the ranking (larger

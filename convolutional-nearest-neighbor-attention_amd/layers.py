@@ -114,7 +114,7 @@ class MultiHeadConvNNAttention(nn.Module):
     def core(self, x):
         """Everything before W_o (layers.py:261-317): returns (z, desc), z the
         merged conv output after dropout.  Under torch.autocast the layer
-        computes in bfloat16 (its kernels' reduced precision); while compiling
+        computes in autocast's dtype (float16 or bfloat16); while compiling
         or under a dispatch mode it runs as the ``cnna::`` library ops and the
         descriptor is a list of ints."""
         if x.dim() != 3:
@@ -189,20 +189,27 @@ class MultiHeadConvNNAttention(nn.Module):
         return y.transpose(1, 2).reshape(B, H, dk, N).permute(0, 3, 1, 2).reshape(B, N, C).contiguous()
 
 
-AMP_DTYPE = torch.bfloat16
-
-
 def _amp_cast(t, dtype):
     return t if t is None or t.dtype == dtype else t.to(dtype)
+
+
+def _amp_dtype():
+    """The reduced type of the active ``torch.autocast('cuda')``: float16 (its
+    default, the reference's ``--use_amp`` loop) or bfloat16."""
+    dt = torch.get_autocast_dtype("cuda")
+    return dt if dt in (torch.float16, torch.bfloat16) else torch.float16
 
 
 def _amp_inputs(x, *weights):
     """Autocast policy of the native layers: inside ``torch.autocast('cuda')``
     (the reference's ``--use_amp`` loop, train_eval.py:137-146) x and the
-    weights are cast to bfloat16, the reduced type the kernels compute in,
-    whatever autocast's own dtype; gradients flow back through the casts."""
+    weights are cast to autocast's dtype (float16 by default, or bfloat16),
+    which the kernels compute in with fp32 accumulation, as autocast runs
+    ``nn.Linear`` and the reference's ``bmm``; gradients flow back through the
+    casts."""
     if torch.is_autocast_enabled("cuda"):
-        return (_amp_cast(x, AMP_DTYPE),) + tuple(_amp_cast(w, AMP_DTYPE) for w in weights)
+        dt = _amp_dtype()
+        return (_amp_cast(x, dt),) + tuple(_amp_cast(w, dt) for w in weights)
     return (x,) + weights
 
 

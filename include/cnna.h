@@ -30,7 +30,11 @@ extern "C" {
 
 #define CNNA_ABI_VERSION 4
 
-enum cnna_dtype { CNNA_F32 = 0, CNNA_BF16 = 1 };
+/* Storage and product type; every kernel accumulates in fp32 (the MFMA
+ * instructions' accumulators) and rounds to nearest-even when it stores.
+ * CNNA_F16 serves torch.autocast(dtype=torch.float16), the reference's AMP
+ * default (train_eval.py:137-146). */
+enum cnna_dtype { CNNA_F32 = 0, CNNA_BF16 = 1, CNNA_F16 = 2 };
 /* magnitude_type (layers.py:167-168, 323-340) */
 enum cnna_metric { CNNA_MATMUL = 0, CNNA_COSINE = 1, CNNA_EUCLIDEAN = 2 };
 /* convolution_type (layers.py:186-228) */

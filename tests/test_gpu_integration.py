@@ -7,7 +7,7 @@
   default backend on a small ViT equals eager;
 * FlopCounterMode counts the registered formulas, forward and backward;
 * under ``torch.autocast('cuda')`` (fp16 by default, as in the reference loop)
-  the layer computes in bfloat16 and its gradients reach the fp32 weights.
+  the layer computes in float16 and its gradients reach the fp32 weights.
 """
 import pytest
 import torch
@@ -107,27 +107,27 @@ def test_flop_counter_counts_forward_and_backward():
     torch.testing.assert_close(y.detach(), m(x).detach(), rtol=1e-5, atol=1e-5)
 
 
-def test_autocast_runs_bf16_and_reaches_fp32_weights():
+def test_autocast_runs_fp16_and_reaches_fp32_weights():
     import copy
     m = _layer(N=128)
-    m16 = copy.deepcopy(m).to(torch.bfloat16)
+    m16 = copy.deepcopy(m).to(torch.float16)
     x = torch.randn(2, 128, 96, device=DEV, requires_grad=True)
     with torch.autocast("cuda"):                     # fp16 autocast, as the reference loop
         y = m(x)
-    assert y.dtype == torch.bfloat16
+    assert y.dtype == torch.float16
     y.float().square().sum().backward()
     assert m.W_q.weight.grad.dtype == torch.float32 and x.grad.dtype == torch.float32
-    # the autocast run is exactly the bfloat16 layer on the rounded inputs and weights
-    x16 = x.detach().to(torch.bfloat16).requires_grad_(True)
+    # the autocast run is exactly the float16 layer on the rounded inputs and weights
+    x16 = x.detach().to(torch.float16).requires_grad_(True)
     y16 = m16(x16)
     y16.float().square().sum().backward()
     assert torch.equal(y, y16)
     for (n, a), (_, b) in zip(m.named_parameters(), m16.named_parameters()):
         assert torch.equal(a.grad, b.grad.float()), n
     assert torch.equal(x.grad, x16.grad.float())
-    # (the bfloat16 layer's own parity is covered by the bf16 parity tests; it
-    # is not compared with the float32 layer here: bf16 rounding of q and k
-    # flips near-tied neighbour choices, which moves whole rows)
+    # (the float16 layer's own parity is covered by tests/test_gpu_fp16.py; it
+    # is not compared with the float32 layer here: rounding q and k flips
+    # near-tied neighbour choices, which moves whole rows)
 
 
 @pytest.mark.parametrize("layer", ["ConvNNAttention", "KvtAttention"])
