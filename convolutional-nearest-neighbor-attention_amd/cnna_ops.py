@@ -48,7 +48,7 @@ class Saved(ctypes.Structure):
 class Grads(ctypes.Structure):
     """Mirror of ``cnna_grads``."""
 
-    _fields_ = [(n, ctypes.c_void_p) for n in ("dx", "dWq", "dWk", "dWv", "dconv_w0", "dconv_w1")]
+    _fields_ = [(n, ctypes.c_void_p) for n in ("dx", "dWq", "dWk", "dWv", "dconv_w0", "dconv_w1", "dbqkv")]
 
 
 class Ln(ctypes.Structure):
@@ -89,7 +89,7 @@ def _load():
         "cnna_row_stats": ([I32, I64, I32, P, I64, P, P], I32),
         "cnna_linear_ln": ([I32, I64, I32, I32, P, I64, ctypes.POINTER(Ln), P, P, I32, P, I64, P, I64, P, P],
                            I32),
-        "cnna_project_qkv_ln": ([D, P, I64, ctypes.POINTER(Ln), P, P, P, P, P, P, P, P, P, P], I32),
+        "cnna_project_qkv_ex": ([D, P, I64, ctypes.POINTER(Ln), P, P, P, P, P, P, P, P, P, P, P], I32),
         "cnna_conv1d_branch_workspace": ([I32] * 6, ctypes.c_size_t),
         "cnna_conv1d_branch": ([I32] * 6 + [P, I64, P, P, P, P, P, P, P, I64, P, ctypes.c_size_t, P], I32),
     }
@@ -110,7 +110,7 @@ EXPORTED = ("cnna_abi_version", "cnna_error_string", "cnna_check_desc", "cnna_he
             "cnna_output_proj", "cnna_forward_workspace", "cnna_forward", "cnna_forward_noalloc",
             "cnna_output_proj_backward_workspace", "cnna_output_proj_backward",
             "cnna_core_backward_workspace", "cnna_core_backward", "cnna_layernorm", "cnna_linear",
-            "cnna_row_stats", "cnna_linear_ln", "cnna_project_qkv_ln",
+            "cnna_row_stats", "cnna_linear_ln", "cnna_project_qkv_ex",
             "cnna_conv1d_branch_workspace", "cnna_conv1d_branch")
 ACT_NONE, ACT_GELU = 0, 1
 
@@ -181,11 +181,12 @@ def _out_rows(out: torch.Tensor, B: int, N: int, C: int) -> int:
     return out.stride(1)
 
 
-def project_qkv(d: Desc, x: torch.Tensor, cand: Optional[torch.Tensor], Wq, Wk, Wv, ln=None):
+def project_qkv(d: Desc, x: torch.Tensor, cand: Optional[torch.Tensor], Wq, Wk, Wv, ln=None, bqkv=None):
     """Returns q (BH,Nq,dkp), k, v (BH,N,dkp), qn, kn (euclidean norms or None).
 
     ``ln``: a :class:`FoldedNorm` of x's rows; the projections then run on
-    LayerNorm(x), normalised as the GEMM loads x (inference only)."""
+    LayerNorm(x), normalised as the GEMM loads x (inference only).
+    ``bqkv``: (3C) [bq | bk | bv] projection biases, or None."""
     x = _token_rows(x)
     ldx = x.stride(1)
     BH, dkp = d.B * d.H, head_stride(d)
@@ -197,15 +198,21 @@ def project_qkv(d: Desc, x: torch.Tensor, cand: Optional[torch.Tensor], Wq, Wk, 
         # euclidean distances need the norms; the cosine backward needs them too
         qn = torch.empty((BH * d.Nq,), dtype=torch.float32, device=x.device)
         kn = torch.empty((BH * d.N,), dtype=torch.float32, device=x.device)
-    if ln is None:
+    if ln is None and bqkv is None:
         check(LIB.cnna_project_qkv(ctypes.byref(d), _ptr(x), ldx, _ptr(cand), _ptr(Wq.contiguous()),
                                    _ptr(Wk.contiguous()), _ptr(Wv.contiguous()), _ptr(q), _ptr(k),
                                    _ptr(v), _ptr(qn), _ptr(kn), _stream()))
     else:
-        ln.check(x)
-        check(LIB.cnna_project_qkv_ln(ctypes.byref(d), _ptr(x), ldx, ctypes.byref(ln.struct()), _ptr(cand),
+        if ln is not None:
+            ln.check(x)
+        if bqkv is not None:
+            if tuple(bqkv.shape) != (3 * d.C,) or bqkv.dtype != x.dtype:
+                raise ValueError(f"cnna: bqkv must be ({3 * d.C},) {x.dtype}, got {tuple(bqkv.shape)} {bqkv.dtype}")
+            bqkv = bqkv.contiguous()
+        check(LIB.cnna_project_qkv_ex(ctypes.byref(d), _ptr(x), ldx,
+                                      None if ln is None else ctypes.byref(ln.struct()), _ptr(cand),
                                       _ptr(Wq.contiguous()), _ptr(Wk.contiguous()), _ptr(Wv.contiguous()),
-                                      _ptr(q), _ptr(k), _ptr(v), _ptr(qn), _ptr(kn), _stream()))
+                                      _ptr(bqkv), _ptr(q), _ptr(k), _ptr(v), _ptr(qn), _ptr(kn), _stream()))
     return q, k, v, qn, kn
 
 
@@ -426,8 +433,10 @@ def output_proj_backward(d: Desc, z, Wo, dout):
     return dz, dWo
 
 
-def core_backward(d: Desc, x, cand, Wq, Wk, Wv, w0, w1, saved, dz):
-    """Gradients of x, W_q, W_k, W_v and the conv weights from dz (B, N, C).
+def core_backward(d: Desc, x, cand, Wq, Wk, Wv, w0, w1, saved, dz, want_db=False):
+    """Gradients of x, W_q, W_k, W_v and the conv weights from dz (B, N, C),
+    and with ``want_db`` that of the projection biases (3C) as a seventh value
+    (None otherwise).
 
     ``saved`` = (q, k, v, qn, kn, idx, vals, w, wmul, cols) from the forward
     stages (wmul: the multipliers applied to w before the aggregation, or None;
@@ -442,15 +451,16 @@ def core_backward(d: Desc, x, cand, Wq, Wk, Wv, w0, w1, saved, dz):
     dWq, dWk, dWv = (torch.empty(W.shape, dtype=x.dtype, device=x.device) for W in (Wq, Wk, Wv))
     dw0 = torch.empty(w0.shape, dtype=x.dtype, device=x.device)
     dw1 = None if w1 is None else torch.empty(w1.shape, dtype=x.dtype, device=x.device)
+    db = torch.empty((3 * d.C,), dtype=x.dtype, device=x.device) if want_db else None
     sv = Saved(*(None if t is None else t.data_ptr() for t in (q, k, v, qn, kn, idx, vals, w, wmul, cols)))
-    gr = Grads(*(None if t is None else t.data_ptr() for t in (dx, dWq, dWk, dWv, dw0, dw1)))
+    gr = Grads(*(None if t is None else t.data_ptr() for t in (dx, dWq, dWk, dWv, dw0, dw1, db)))
     nws = LIB.cnna_core_backward_workspace(ctypes.byref(d))
     ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=x.device)
     check(LIB.cnna_core_backward(ctypes.byref(d), _ptr(x), x.stride(1), _ptr(cand),
                                  _ptr(Wq.contiguous()), _ptr(Wk.contiguous()), _ptr(Wv.contiguous()),
                                  _ptr(w0c), _ptr(w1c), ctypes.byref(sv), _ptr(dz), ctypes.byref(gr),
                                  _ptr(ws), nws, _stream()))
-    return dx, dWq, dWk, dWv, dw0, dw1
+    return dx, dWq, dWk, dWv, dw0, dw1, db
 
 
 # --------------------------------------------------------------------------
@@ -470,16 +480,21 @@ class ConvNNCore(torch.autograd.Function):
     drawn over the whole score matrix (MultiHeadKvtAttention's ``attn_drop``,
     layers.py:680); the kept probabilities are multiplied by
     ``dmask[..., idx] * dscale`` (0 or 1/(1-p)); depthwise conv only.
+
+    ``bqkv``: optional (3C) [bq | bk | bv] projection biases
+    (MultiHeadKvtAttention's ``qkv_bias``, layers.py:662).
     """
 
     @staticmethod
-    def forward(ctx, x, Wq, Wk, Wv, w0, w1, cand, d, reference_errors=False, dmask=None, dscale=1.0):
-        q, k, v, qn, kn = project_qkv(d, x, cand, Wq, Wk, Wv)
+    def forward(ctx, x, Wq, Wk, Wv, w0, w1, cand, d, reference_errors=False, dmask=None, dscale=1.0,
+                bqkv=None):
+        q, k, v, qn, kn = project_qkv(d, x, cand, Wq, Wk, Wv, bqkv=bqkv)
         idx, vals, w, cols = select_cols(d, k, q, kn, qn, cand)
         wmul = entry_multipliers(d, idx, dmask, dscale)
         z = aggregate(d, v, idx, w if wmul is None else w * wmul, w0, w1)
         ctx.d = d
         ctx.reference_errors = reference_errors
+        ctx.has_bias = bqkv is not None
         ctx.save_for_backward(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul, cols)
         return z
 
@@ -492,11 +507,12 @@ class ConvNNCore(torch.autograd.Function):
                 "inplace operation: the sampled euclidean similarity is masked in place after "
                 "sqrt (layers.py:291-292, 304-305)")
         x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul, cols = ctx.saved_tensors
-        dx, dWq, dWk, dWv, dw0, dw1 = core_backward(ctx.d, x, cand, Wq, Wk, Wv, w0, w1,
-                                                    (q, k, v, qn, kn, idx, vals, w, wmul, cols), dz)
+        dx, dWq, dWk, dWv, dw0, dw1, db = core_backward(ctx.d, x, cand, Wq, Wk, Wv, w0, w1,
+                                                        (q, k, v, qn, kn, idx, vals, w, wmul, cols), dz,
+                                                        want_db=ctx.has_bias)
         dw0 = dw0.to(w0.dtype)
         dw1 = None if dw1 is None else dw1.to(w1.dtype)
-        return dx, dWq, dWk, dWv, dw0, dw1, None, None, None, None, None
+        return dx, dWq, dWk, dWv, dw0, dw1, None, None, None, None, None, db
 
 
 def entry_multipliers(d: Desc, idx, dmask, dscale):
@@ -572,15 +588,17 @@ _EMPTY = lambda like: torch.empty((0,), dtype=torch.float32, device=like.device)
 @torch.library.custom_op("cnna::core", mutates_args=())
 def core_op(x: torch.Tensor, Wq: torch.Tensor, Wk: torch.Tensor, Wv: torch.Tensor, w0: torch.Tensor,
             w1: Optional[torch.Tensor], cand: Optional[torch.Tensor], dmask: Optional[torch.Tensor],
-            desc: List[int], scale: float, reference_errors: bool, dscale: float
+            desc: List[int], scale: float, reference_errors: bool, dscale: float,
+            bqkv: Optional[torch.Tensor] = None
             ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
                        torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """x -> (z, q, k, v, qn, kn, idx, vals, w, wmul, cols): projections,
-    selection, aggregation, head merge (layers.py:261-317); qn / kn empty when
-    unused; wmul the per-entry dropout multipliers of ``dmask`` (empty
-    without); cols the sampled paths' candidate columns (empty for 'all')."""
+    """x -> (z, q, k, v, qn, kn, idx, vals, w, wmul, cols): projections (with
+    the optional (3C) biases ``bqkv``), selection, aggregation, head merge
+    (layers.py:261-317); qn / kn empty when unused; wmul the per-entry dropout
+    multipliers of ``dmask`` (empty without); cols the sampled paths'
+    candidate columns (empty for 'all')."""
     d = _desc_of(desc, scale)
-    q, k, v, qn, kn = project_qkv(d, x, cand, Wq, Wk, Wv)
+    q, k, v, qn, kn = project_qkv(d, x, cand, Wq, Wk, Wv, bqkv=bqkv)
     idx, vals, w, cols = select_cols(d, k, q, kn, qn, cand)
     wmul = entry_multipliers(d, idx, dmask, dscale)
     z = aggregate(d, v, idx, w if wmul is None else w * wmul, w0, w1)
@@ -590,7 +608,7 @@ def core_op(x: torch.Tensor, Wq: torch.Tensor, Wk: torch.Tensor, Wv: torch.Tenso
 
 
 @core_op.register_fake
-def _core_fake(x, Wq, Wk, Wv, w0, w1, cand, dmask, desc, scale, reference_errors, dscale):
+def _core_fake(x, Wq, Wk, Wv, w0, w1, cand, dmask, desc, scale, reference_errors, dscale, bqkv=None):
     B, N, C, H, Nq, K = desc[:6]
     BH, dkp = B * H, _dkp(desc)
     f32 = dict(dtype=torch.float32, device=x.device)
@@ -608,32 +626,38 @@ def core_backward_op(x: torch.Tensor, Wq: torch.Tensor, Wk: torch.Tensor, Wv: to
                      w0: torch.Tensor, w1: Optional[torch.Tensor], cand: Optional[torch.Tensor],
                      q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qn: torch.Tensor, kn: torch.Tensor,
                      idx: torch.Tensor, vals: torch.Tensor, w: torch.Tensor, wmul: Optional[torch.Tensor],
-                     cols: Optional[torch.Tensor], dz: torch.Tensor, desc: List[int], scale: float
+                     cols: Optional[torch.Tensor], dz: torch.Tensor, desc: List[int], scale: float,
+                     want_db: bool = False
                      ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
-                                torch.Tensor]:
-    """Gradients (dx, dWq, dWk, dWv, dw0, dw1) of ``cnna::core``; dw1 empty without w1."""
+                                torch.Tensor, torch.Tensor]:
+    """Gradients (dx, dWq, dWk, dWv, dw0, dw1, dbqkv) of ``cnna::core``; dw1
+    empty without w1, dbqkv empty without ``want_db``."""
     d = _desc_of(desc, scale)
     nq = None if qn.numel() == 0 else qn
     nk = None if kn.numel() == 0 else kn
-    dx, dWq, dWk, dWv, dw0, dw1 = core_backward(d, x, cand, Wq, Wk, Wv, w0, w1,
-                                                (q, k, v, nq, nk, idx, vals, w, wmul, cols), dz)
-    return dx, dWq, dWk, dWv, dw0.to(w0.dtype), (x.new_empty((0,)) if dw1 is None else dw1.to(w1.dtype))
+    dx, dWq, dWk, dWv, dw0, dw1, db = core_backward(d, x, cand, Wq, Wk, Wv, w0, w1,
+                                                    (q, k, v, nq, nk, idx, vals, w, wmul, cols), dz,
+                                                    want_db=want_db)
+    return (dx, dWq, dWk, dWv, dw0.to(w0.dtype), (x.new_empty((0,)) if dw1 is None else dw1.to(w1.dtype)),
+            x.new_empty((0,)) if db is None else db)
 
 
 @core_backward_op.register_fake
 def _core_backward_fake(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul, cols, dz, desc,
-                        scale):
+                        scale, want_db=False):
     return (x.new_empty(x.shape), x.new_empty(Wq.shape), x.new_empty(Wk.shape), x.new_empty(Wv.shape),
-            w0.new_empty(w0.shape), (x.new_empty((0,)) if w1 is None else w1.new_empty(w1.shape)))
+            w0.new_empty(w0.shape), (x.new_empty((0,)) if w1 is None else w1.new_empty(w1.shape)),
+            x.new_empty((3 * desc[2],) if want_db else (0,)))
 
 
 def _core_setup(ctx, inputs, output):
-    x, Wq, Wk, Wv, w0, w1, cand, dmask, desc, scale, reference_errors, dscale = inputs
+    x, Wq, Wk, Wv, w0, w1, cand, dmask, desc, scale, reference_errors, dscale, bqkv = inputs
     z, q, k, v, qn, kn, idx, vals, w, wmul, cols = output
     wmul = None if dmask is None else wmul
     cols = cols if desc[11] else None
     ctx.desc, ctx.scale, ctx.reference_errors = desc, scale, reference_errors
     ctx.has_w1 = w1 is not None
+    ctx.has_bias = bqkv is not None
     ctx.save_for_backward(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul, cols)
 
 
@@ -645,9 +669,11 @@ def _core_bwd(ctx, dz, *unused):
             "inplace operation: the sampled euclidean similarity is masked in place after "
             "sqrt (layers.py:291-292, 304-305)")
     x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx, vals, w, wmul, cols = ctx.saved_tensors
-    dx, dWq, dWk, dWv, dw0, dw1 = core_backward_op(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx,
-                                                   vals, w, wmul, cols, dz.contiguous(), dl, ctx.scale)
-    return dx, dWq, dWk, dWv, dw0, (dw1 if ctx.has_w1 else None), None, None, None, None, None, None
+    dx, dWq, dWk, dWv, dw0, dw1, db = core_backward_op(x, Wq, Wk, Wv, w0, w1, cand, q, k, v, qn, kn, idx,
+                                                       vals, w, wmul, cols, dz.contiguous(), dl, ctx.scale,
+                                                       ctx.has_bias)
+    return (dx, dWq, dWk, dWv, dw0, (dw1 if ctx.has_w1 else None), None, None, None, None, None, None,
+            db if ctx.has_bias else None)
 
 
 torch.library.register_autograd("cnna::core", _core_bwd, setup_context=_core_setup)

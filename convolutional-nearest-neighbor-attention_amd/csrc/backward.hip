@@ -942,6 +942,25 @@ __global__ __launch_bounds__(256) void scatter_rows_kernel(const T* dxs, const i
   }
 }
 
+// Column sums (the bias gradient of the projections): 32 columns per block,
+// 32 row groups strided over the rows, the group partials added in order.
+template <typename T>
+__global__ __launch_bounds__(1024) void colsum_kernel(const T* a, int64_t rows, int cols, int64_t lda, T* out) {
+  __shared__ float part[32][33];
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  const int c = blockIdx.x * 32 + tx;
+  float s = 0.0f;
+  if (c < cols)
+    for (int64_t r = ty; r < rows; r += 32) s += ldf(a + r * lda + c);
+  part[ty][tx] = s;
+  __syncthreads();
+  if (ty == 0 && c < cols) {
+    float t = 0.0f;
+    for (int i = 0; i < 32; ++i) t += part[i][tx];
+    stf(out + c, t);
+  }
+}
+
 inline dim3 grid_for(int64_t n) { return dim3((unsigned)((n + 255) / 256)); }
 
 }  // namespace
@@ -1074,6 +1093,23 @@ int launch_scatter_rows(int dtype, const void* dxs, const int32_t* cand, void* d
   else if (dtype == CNNA_F32)
     hipLaunchKernelGGL(scatter_rows_kernel<float>, grid_for(n), dim3(256), 0, s,
                        static_cast<const float*>(dxs), cand, static_cast<float*>(dx), B, N, Nq, C);
+  else
+    return CNNA_ERR_DTYPE;
+  return (int)hipGetLastError();
+}
+
+int launch_colsum(int dtype, const void* a, int64_t rows, int cols, int64_t lda, void* out, hipStream_t s) {
+  if (cols <= 0) return 0;
+  const dim3 grid((unsigned)((cols + 31) / 32));
+  if (dtype == CNNA_BF16)
+    hipLaunchKernelGGL(colsum_kernel<uint16_t>, grid, dim3(1024), 0, s, static_cast<const uint16_t*>(a), rows,
+                       cols, lda, static_cast<uint16_t*>(out));
+  else if (dtype == CNNA_F16)
+    hipLaunchKernelGGL(colsum_kernel<_Float16>, grid, dim3(1024), 0, s, static_cast<const _Float16*>(a), rows,
+                       cols, lda, static_cast<_Float16*>(out));
+  else if (dtype == CNNA_F32)
+    hipLaunchKernelGGL(colsum_kernel<float>, grid, dim3(1024), 0, s, static_cast<const float*>(a), rows, cols,
+                       lda, static_cast<float*>(out));
   else
     return CNNA_ERR_DTYPE;
   return (int)hipGetLastError();

@@ -85,8 +85,8 @@ int set_ln(GemmArgs& g, const cnna_ln* ln) {
 }
 
 int project_qkv_impl(const cnna_desc* d, const void* x, int64_t ldx, const cnna_ln* ln, const int32_t* cand,
-                     const void* Wq, const void* Wk, const void* Wv, void* q, void* k, void* v,
-                     float* qn, float* kn, void* stream) {
+                     const void* Wq, const void* Wk, const void* Wv, const void* bqkv, void* q, void* k,
+                     void* v, float* qn, float* kn, void* stream) {
   int st = cnna_check_desc(d);
   if (st) return st;
   if (!x || !Wq || !Wk || !Wv || !q || !k || !v) return CNNA_ERR_NULL;
@@ -116,6 +116,7 @@ int project_qkv_impl(const cnna_desc* d, const void* x, int64_t ldx, const cnna_
     g.w[0] = Wq; g.w[1] = Wk; g.w[2] = Wv;
     g.o[0] = q; g.o[1] = k; g.o[2] = v;
     g.o_rows = d->N;
+    g.bias = bqkv;
     if ((st = launch_gemm(d->dtype, GEMM_A_ROWS, GEMM_O_HEADSPLIT, g, s))) return st;
   } else {
     g.M = d->B * d->N;
@@ -123,11 +124,13 @@ int project_qkv_impl(const cnna_desc* d, const void* x, int64_t ldx, const cnna_
     g.w[0] = Wk; g.w[1] = Wv;
     g.o[0] = k; g.o[1] = v;
     g.o_rows = d->N;
+    g.bias = bqkv ? static_cast<const char*>(bqkv) + (size_t)d->C * es : nullptr;
     if ((st = launch_gemm(d->dtype, GEMM_A_ROWS, GEMM_O_HEADSPLIT, g, s))) return st;
     // Q on the sampled tokens x[:, cand, :] (layers.py:285-286, 298-299)
     g.M = d->B * d->Nq;
     g.Nc = d->C;
     g.w[0] = Wq; g.o[0] = q;
+    g.bias = bqkv;
     g.arow = cand;
     g.a_rows = d->Nq;
     g.a_src_rows = d->N;
@@ -162,14 +165,13 @@ extern "C" {
 int cnna_project_qkv(const cnna_desc* d, const void* x, int64_t ldx, const int32_t* cand,
                      const void* Wq, const void* Wk, const void* Wv, void* q, void* k, void* v,
                      float* qn, float* kn, void* stream) {
-  return project_qkv_impl(d, x, ldx, nullptr, cand, Wq, Wk, Wv, q, k, v, qn, kn, stream);
+  return project_qkv_impl(d, x, ldx, nullptr, cand, Wq, Wk, Wv, nullptr, q, k, v, qn, kn, stream);
 }
 
-int cnna_project_qkv_ln(const cnna_desc* d, const void* x, int64_t ldx, const cnna_ln* ln,
-                        const int32_t* cand, const void* Wq, const void* Wk, const void* Wv, void* q,
-                        void* k, void* v, float* qn, float* kn, void* stream) {
-  if (!ln) return CNNA_ERR_NULL;
-  return project_qkv_impl(d, x, ldx, ln, cand, Wq, Wk, Wv, q, k, v, qn, kn, stream);
+int cnna_project_qkv_ex(const cnna_desc* d, const void* x, int64_t ldx, const cnna_ln* ln,
+                        const int32_t* cand, const void* Wq, const void* Wk, const void* Wv,
+                        const void* bqkv, void* q, void* k, void* v, float* qn, float* kn, void* stream) {
+  return project_qkv_impl(d, x, ldx, ln, cand, Wq, Wk, Wv, bqkv, q, k, v, qn, kn, stream);
 }
 
 int cnna_select(const cnna_desc* d, const void* k, const void* q, const float* kn, const float* qn,

@@ -276,6 +276,18 @@ int cnna_core_backward(const cnna_desc* d, const void* x, int64_t ldx, const int
     if ((st = launch_pull(dt, pa, s))) return st;
   }
 
+  // bias gradients of the projections: column sums of dQ, dK, dV
+  if (gr->dbqkv != nullptr) {
+    char* db = static_cast<char*>(gr->dbqkv);
+    const size_t es = elem_size(dt);
+    if (!d->sampled) {
+      if ((st = launch_colsum(dt, p.dqkv, (int64_t)B * N, 3 * C, ld3, db, s))) return st;
+    } else {
+      if ((st = launch_colsum(dt, p.dqkv, (int64_t)B * N, 2 * C, ld3, db + C * es, s))) return st;
+      if ((st = launch_colsum(dt, p.dqs, (int64_t)B * Nq, C, C, db, s))) return st;
+    }
+  }
+
   // 5. projections: dx and the weight gradients.  dx = dqkv @ [W_q; W_k; W_v]
   // as a row GEMM against the transposed stack (the forward kernel)
   {

@@ -539,8 +539,11 @@ int launch_x(int omode, const GemmArgs& g, hipStream_t s, dim3 grid) {
   // LayerNorm prologue and / or statistics epilogue (row-major A)
   const int xf = (g.ln_stats ? 1 : 0) | (g.st_out ? 2 : 0);
   if (omode == GEMM_O_HEADSPLIT) {
-    if (xf != 1 || g.bias || g.res || g.act != GEMM_ACT_NONE) return CNNA_ERR_OPTION;
-    hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_HEADSPLIT, FAST, 0, 1>), grid, dim3(256), 0, s, g);
+    if (xf != 1 || g.res || g.act != GEMM_ACT_NONE) return CNNA_ERR_OPTION;
+    if (g.bias)
+      hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_HEADSPLIT, FAST, 1, 1>), grid, dim3(256), 0, s, g);
+    else
+      hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_HEADSPLIT, FAST, 0, 1>), grid, dim3(256), 0, s, g);
     return (int)hipGetLastError();
   }
   const bool gelu = g.act == GEMM_ACT_GELU;
@@ -576,7 +579,11 @@ int launch_f(int amode, int omode, const GemmArgs& g, hipStream_t s) {
     if (g.ln_stats && g.Kd > LN_MAX_K) return CNNA_ERR_UNSUPPORTED;
     return launch_x<T, FAST>(omode, g, s, grid);
   }
-  if (amode == GEMM_A_ROWS && omode == GEMM_O_HEADSPLIT)
+  if (amode == GEMM_A_ROWS && omode == GEMM_O_HEADSPLIT && (g.res || g.act != GEMM_ACT_NONE))
+    return CNNA_ERR_OPTION;   // the head split takes a bias only
+  else if (amode == GEMM_A_ROWS && omode == GEMM_O_HEADSPLIT && g.bias)
+    hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_HEADSPLIT, FAST, 1>), grid, dim3(256), 0, s, g);
+  else if (amode == GEMM_A_ROWS && omode == GEMM_O_HEADSPLIT)
     hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_HEADSPLIT, FAST>), grid, dim3(256), 0, s, g);
   else if (amode == GEMM_A_ROWS && omode == GEMM_O_PLAIN && g.act == GEMM_ACT_GELU)
     hipLaunchKernelGGL((gemm_kernel<T, GEMM_A_ROWS, GEMM_O_PLAIN, FAST, 2>), grid, dim3(256), 0, s, g);

@@ -31,13 +31,13 @@ struct GemmArgs {
   int o_rows, o_H, o_dk, o_dkp;
   int avec, bvec;  // 16-byte vector loads allowed for A / W
   int ovec;        // set by the launcher: 4-column vector stores allowed
-  int ostage;      // set by the launcher: bf16 tile staged through LDS for 16-byte stores
-  // plain output only (nn.Linear extras): out = act(A W^T + bias) + res
-  const void* bias;  // (Nc) or NULL
+  int ostage;      // set by the launcher: 16-bit tile staged through LDS for 16-byte stores
+  // nn.Linear extras: out = act(A W^T + bias) + res (act and res: plain output only)
+  const void* bias;  // (Nc) or NULL, indexed by the stacked output column
   int act;           // GEMM_ACT_*
   const void* res;   // (M, Nc) residual with row stride ldr, or NULL
   int64_t ldr;
-  // prologue (bf16, row-major A): A rows are LayerNorm-ed on load,
+  // prologue (row-major A): A rows are LayerNorm-ed on load,
   //   a[m][k] = round((x[m][k] - mean_m) * rstd_m * gamma[k] + beta[k]),
   // mean_m / rstd_m combined from ln_parts per-tile (mean, M2) partials of
   // the row (ROW_STAT_TILE columns each, the last one partial), or NULL
@@ -46,7 +46,7 @@ struct GemmArgs {
   const void* ln_gamma;
   const void* ln_beta;
   float ln_eps;
-  // epilogue (staged bf16, plain output): per ROW_STAT_TILE-column tile of
+  // epilogue (staged 16-bit, plain output): per ROW_STAT_TILE-column tile of
   // each output row, (mean, M2) of the stored values, at
   // st_out[(m * ceil(Nc / ROW_STAT_TILE) + tile) * 2], or NULL
   float* st_out;
@@ -78,6 +78,8 @@ struct LnArgs {
   // prologue's format), or NULL
   float* stats;
 };
+// deterministic column sums out[c] = sum_r a[r * lda + c] (fp32, fixed order), rounded to the dtype
+int launch_colsum(int dtype, const void* a, int64_t rows, int cols, int64_t lda, void* out, hipStream_t s);
 int launch_layernorm(int dtype, const LnArgs& a, hipStream_t s);
 
 // ---------------------------------------------------------------- prep

@@ -440,8 +440,9 @@ class MultiHeadKvtAttention(nn.Module):
     the reference's dense (B, H, N, N) mask and applies it at the kept
     probabilities (the dropped entries of the reference's dense row are zero
     already).  Any ``topk`` runs forward (selections wider than 32 in rounds
-    of 32); the backward takes ``topk`` <= 64; ``qkv_bias`` is not supported
-    (NotImplementedError otherwise).
+    of 32); the backward takes ``topk`` <= 64 (NotImplementedError otherwise).
+    ``qkv_bias`` adds the biases in the
+    projection GEMM's epilogue; their gradient is the column sums of dQ, dK, dV.
     """
 
     def __init__(self, dim, num_heads=8, qkv_bias=False, qk_scale=None, attn_drop=0., proj_drop=0.,
@@ -472,13 +473,13 @@ class MultiHeadKvtAttention(nn.Module):
     def forward(self, x):
         if not x.is_cuda:
             raise RuntimeError("MultiHeadKvtAttention (cnna) runs on ROCm device tensors only")
-        if self.qkv.bias is not None:
-            raise NotImplementedError("cnna: MultiHeadKvtAttention with qkv_bias")
         B, N, C = x.shape
         H = self.num_heads
         if self.topk > N:
             raise RuntimeError("selected index k out of range")                # torch.topk
-        x, W, P = _amp_inputs(x, self.qkv.weight, self.proj.weight)
+        x, W, P, b = _amp_inputs(x, self.qkv.weight, self.proj.weight, self.qkv.bias)
+        # qkv_bias (layers.py:662) in this operator's role order [W_q | W_k | W_v]
+        bqkv = None if b is None else torch.cat((b[C:2 * C], b[:C], b[2 * C:]))
         if W.dtype != x.dtype:
             raise RuntimeError(f"mat1 and mat2 must have the same dtype, but got {x.dtype} and "
                                f"{W.dtype}")
@@ -488,9 +489,10 @@ class MultiHeadKvtAttention(nn.Module):
             d = ops.desc_values(B, N, C, H, N, self.topk, N, x.dtype, "matmul", "depthwise", True, False,
                                 False, merge=ops.MERGE_CONCAT)
             z = torch.ops.cnna.core(x, W[C:2 * C], W[:C], W[2 * C:], ones, None, None, dmask, d,
-                                    float(self.scale), False, dscale)[0]
+                                    float(self.scale), False, dscale, bqkv)[0]
             return self.proj_drop(torch.ops.cnna.output_proj(z, P, d, float(self.scale)))
         d = ops.make_desc(B, N, C, H, N, self.topk, N, x.dtype, "matmul", "depthwise", True, False, False,
                           merge=ops.MERGE_CONCAT, scale=self.scale)
-        z = ops.ConvNNCore.apply(x, W[C:2 * C], W[:C], W[2 * C:], ones, None, None, d, False, dmask, dscale)
+        z = ops.ConvNNCore.apply(x, W[C:2 * C], W[:C], W[2 * C:], ones, None, None, d, False, dmask, dscale,
+                                 bqkv)
         return self.proj_drop(ops.OutputProj.apply(z, P, d))

@@ -18,7 +18,7 @@ residual, fc2 + residual) also writes the row's statistics in its epilogue
 (bf16; fp32 takes a statistics pass over the row instead), and the GEMM that
 consumes the row (the next block's Q/K/V projection, fc1) normalises it as it
 loads it; the first block's statistics come from a pre-pass (cnna_row_stats,
-cnna_linear_ln, cnna_project_qkv_ln).  Other layers keep a LayerNorm kernel in
+cnna_linear_ln, cnna_project_qkv_ex).  Other layers keep a LayerNorm kernel in
 front of the attention and the residual add inside the second LayerNorm.
 fc1 + bias + GELU and fc2 + bias + residual are GEMM epilogues throughout.
 Training and autograd use the composable modules.

@@ -211,6 +211,10 @@ typedef struct cnna_grads {
   void* dWv;
   void* dconv_w0;
   void* dconv_w1;
+  /* (3C) [dbq | dbk | dbv]: gradient of the projection biases of
+   * cnna_project_qkv_ex (MultiHeadKvtAttention's qkv_bias, layers.py:662), or
+   * NULL when the projections have no bias */
+  void* dbqkv;
 } cnna_grads;
 
 /* Backward of cnna_output_proj (nn.Linear W_o, layers.py:320):
@@ -268,7 +272,7 @@ int cnna_linear(int32_t dtype, int64_t M, int32_t Nout, int32_t Kd, const void* 
  *    or, for the first block, cnna_row_stats;
  *  - the normalisation (x - mean) / sqrt(var + eps) * gamma + beta, rounded to
  *    the dtype as nn.LayerNorm's output is, applied by the consuming GEMM
- *    (cnna_linear_ln, cnna_project_qkv_ln) as it loads each row.
+ *    (cnna_linear_ln, cnna_project_qkv_ex) as it loads each row.
  * The statistics are fp32 partials, stats[(row * CNNA_STAT_PARTS(C) + t) * 2
  * + {0, 1}] = the mean and the sum of squared deviations from that mean of the
  * row's columns [128 t, min(128 (t + 1), C)); mean and var (biased, as
@@ -298,13 +302,17 @@ int cnna_linear_ln(int32_t dtype, int64_t M, int32_t Nout, int32_t Kd, const voi
                    const cnna_ln* ln, const void* W, const void* bias, int32_t act, const void* res,
                    int64_t ldr, void* out, int64_t ldo, float* stats_out, void* stream);
 
-/* cnna_project_qkv on LayerNorm(x) (vit.py:262 feeding layers.py:264-265):
- * the rows of x are normalised with ln (C = d->C; stats indexed by the row
- * b * N + t of x, also for the sampled Q rows) as the projection GEMM loads
- * them.  ln is required. */
-int cnna_project_qkv_ln(const cnna_desc* d, const void* x, int64_t ldx, const cnna_ln* ln,
-                        const int32_t* cand, const void* Wq, const void* Wk, const void* Wv, void* q,
-                        void* k, void* v, float* qn, float* kn, void* stream);
+/* cnna_project_qkv with two optional extras:
+ *  ln    LayerNorm(x) instead of x (vit.py:262 feeding layers.py:264-265): the
+ *        rows of x are normalised (C = d->C; stats indexed by the row b * N + t
+ *        of x, also for the sampled Q rows) as the projection GEMM loads them;
+ *        NULL: x itself;
+ *  bqkv  (3C) [bq | bk | bv] biases added to the projections (nn.Linear with
+ *        bias: MultiHeadKvtAttention's qkv_bias, layers.py:662, in this
+ *        operator's role order); NULL: none. */
+int cnna_project_qkv_ex(const cnna_desc* d, const void* x, int64_t ldx, const cnna_ln* ln,
+                        const int32_t* cand, const void* Wq, const void* Wk, const void* Wv,
+                        const void* bqkv, void* q, void* k, void* v, float* qn, float* kn, void* stream);
 
 /* ---- branching callers (layers.py:502-652) ----
  * MultiHeadConv1dAttention (layers.py:452-499), the Conv1d branch of

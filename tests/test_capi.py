@@ -179,8 +179,8 @@ def test_folded_layernorm_limits():
     assert lin(ops.CNNA_BF16, 64, 192, 192, fake, 192, ctypes.byref(bad), fake, None, 0, None, 0, fake, 192,
                None, None) == ops.ERR_NULL
     d = desc(dtype=ops.CNNA_BF16)
-    assert ops.LIB.cnna_project_qkv_ln(ctypes.byref(d), fake, 12, None, None, fake, fake, fake, fake, fake,
-                                       fake, None, None, None) == ops.ERR_NULL
+    assert ops.LIB.cnna_project_qkv_ex(ctypes.byref(d), fake, 12, ctypes.byref(bad), None, fake, fake, fake,
+                                       None, fake, fake, fake, None, None, None) == ops.ERR_NULL
     assert ops.LIB.cnna_row_stats(ops.CNNA_BF16, 4, 192, fake, 100, st, None) == ops.ERR_SHAPE
     assert ops.LIB.cnna_row_stats(ops.CNNA_BF16, 0, 192, None, 192, None, None) == 0
     assert b"folded LayerNorm" in ops.LIB.cnna_error_string(ops.ERR_UNSUPPORTED)

@@ -8,7 +8,7 @@
   through the composable modules;
 * the folded LayerNorm: cnna_row_stats's per-tile (mean, M2) partials equal
   the float64 ones; the GEMMs' LayerNorm prologue equals LayerNorm -> GEMM
-  (cnna_linear_ln, cnna_project_qkv_ln, also on the sampled Q rows); the
+  (cnna_linear_ln, cnna_project_qkv_ex, also on the sampled Q rows); the
   statistics epilogue equals the statistics pass over the stored output; a
   folded ViT block runs no LayerNorm kernel.
 """

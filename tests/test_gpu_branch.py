@@ -155,16 +155,21 @@ def test_branching_conv_backward_through_slice():
         torch.testing.assert_close(a.grad.double().cpu(), b.grad, rtol=2e-3, atol=2e-3, msg=n)
 
 
-def _kvt(dtype, C=192, H=3, topk=9, attn_drop=0.0, qk_scale=None):
+def _kvt(dtype, C=192, H=3, topk=9, attn_drop=0.0, qk_scale=None, qkv_bias=False):
     torch.manual_seed(11)
-    return MultiHeadKvtAttention(C, num_heads=H, attn_drop=attn_drop, qk_scale=qk_scale,
-                                 topk=topk).to(DEV).to(dtype).eval()
+    m = MultiHeadKvtAttention(C, num_heads=H, attn_drop=attn_drop, qk_scale=qk_scale, topk=topk,
+                              qkv_bias=qkv_bias).to(DEV)
+    if qkv_bias:
+        with torch.no_grad():
+            m.qkv.bias.copy_(torch.randn(3 * C, device=DEV) * 0.5)
+    return m.to(dtype).eval()
 
 
 def _kvt_oracle(m, x, wmul=None):
     H = m.num_heads
     return O.kvt(_cpu(x), _cpu(m.qkv.weight), _cpu(m.proj.weight), H, m.topk, m.scale,
-                 wmul=None if wmul is None else wmul.double().cpu())
+                 wmul=None if wmul is None else wmul.double().cpu(),
+                 bqkv=None if m.qkv.bias is None else _cpu(m.qkv.bias))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -216,8 +221,6 @@ def test_kvt_errors():
     y = m(x)
     with pytest.raises(NotImplementedError, match="K <= 64"):
         y.sum().backward()
-    with pytest.raises(NotImplementedError):
-        MultiHeadKvtAttention(64, 2, qkv_bias=True, topk=4).to(DEV)(torch.randn(1, 8, 64, device=DEV))
 
 
 @pytest.mark.parametrize("H,topk", [(1, 9), (3, 9), (3, 48), (2, 64)])
@@ -273,3 +276,71 @@ def test_vit_layers_fused_match_composable(layer):
     with torch.enable_grad():
         plain = model(imgs).detach()
     torch.testing.assert_close(fused, plain, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_kvt_qkv_bias_forward(dtype):
+    """qkv_bias=True (layers.py:662): the biases go into the projection GEMM's
+    epilogue in the operator's role order."""
+    B, N, C, H, topk = 3, 197, 96, 3, 9
+    m = _kvt(dtype, C, H, topk, qkv_bias=True)
+    x = torch.randn(B, N, C, device=DEV).to(dtype)
+    with torch.no_grad():
+        got = m(x)
+    if dtype == torch.float32:
+        torch.testing.assert_close(got.double().cpu(), _kvt_oracle(m, x), rtol=1e-3, atol=1e-3)
+        return
+    # bf16: the kernel's own projections equal x W^T + b rounded, and the
+    # output is the exact aggregation over the kernel's selection
+    W, b = m.qkv.weight, m.qkv.bias
+    bq = torch.cat((b[C:2 * C], b[:C], b[2 * C:]))
+    d = ops.make_desc(B, N, C, H, N, topk, N, dtype, "matmul", "depthwise", True, False, False,
+                      merge=ops.MERGE_CONCAT, scale=m.scale)
+    with torch.no_grad():
+        q, k, v, _, _ = ops.project_qkv(d, x, None, W[C:2 * C], W[:C], W[2 * C:], bqkv=bq)
+    dk = C // H
+    ref_k = (x.float() @ W[:C].float().t() + b[:C].float()).view(B, N, H, dk).transpose(1, 2).reshape(B * H, N, dk)
+    torch.testing.assert_close(k[..., :dk].float(), ref_k, rtol=1e-2, atol=1e-2)
+    with torch.no_grad():
+        idx, vals, w = ops.select(d, k, q)
+    rows, cands, vv = (t[..., :dk].double().cpu() for t in (k, q, v))
+    S = torch.matmul(rows, cands.transpose(1, 2)) * m.scale
+    _, idx_e = O.stable_topk(S, topk, largest=True)
+    idx_g = idx.long().cpu()
+    assert O.topk_gap_ok(S, idx_g, idx_e, O.Config(d_hidden=C, num_heads=H, K=topk), tol=1e-6).all()
+    pr = torch.softmax(torch.gather(S, -1, idx_g), -1)
+    o = (pr.unsqueeze(-1) * vv[torch.arange(B * H).view(-1, 1, 1), idx_g]).sum(2)
+    z = o.view(B, H, N, dk).transpose(1, 2).reshape(B, N, C).to(dtype).double()
+    torch.testing.assert_close(got.double().cpu(), z @ _cpu(m.proj.weight).T, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("topk", [9, 40])
+def test_kvt_qkv_bias_backward(topk):
+    m = _kvt(torch.float32, 96, 3, topk=topk, qkv_bias=True).train()
+    x = torch.randn(2, 197, 96, device=DEV, requires_grad=True)
+    m(x).square().sum().backward()
+    xc = x.detach().double().cpu().requires_grad_(True)
+    Wqkv = m.qkv.weight.detach().double().cpu().requires_grad_(True)
+    bqkv = m.qkv.bias.detach().double().cpu().requires_grad_(True)
+    Wp = m.proj.weight.detach().double().cpu().requires_grad_(True)
+    O.kvt(xc, Wqkv, Wp, 3, topk, m.scale, bqkv=bqkv).square().sum().backward()
+    torch.testing.assert_close(x.grad.double().cpu(), xc.grad, rtol=2e-3, atol=2e-3)
+    torch.testing.assert_close(m.qkv.weight.grad.double().cpu(), Wqkv.grad, rtol=2e-3, atol=2e-3)
+    torch.testing.assert_close(m.qkv.bias.grad.double().cpu(), bqkv.grad, rtol=2e-3, atol=2e-3)
+    torch.testing.assert_close(m.proj.weight.grad.double().cpu(), Wp.grad, rtol=2e-3, atol=2e-3)
+
+
+def test_kvt_qkv_bias_compiled_matches_eager():
+    m = _kvt(torch.float32, 96, 3, topk=9, qkv_bias=True).train()
+    x = torch.randn(2, 100, 96, device=DEV, requires_grad=True)
+    y = m(x)
+    y.square().sum().backward()
+    g_eager = (x.grad.clone(), m.qkv.bias.grad.clone())
+    x.grad = None
+    m.zero_grad()
+    mc = torch.compile(m, fullgraph=True)
+    yc = mc(x)
+    yc.square().sum().backward()
+    torch.testing.assert_close(yc, y, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(x.grad, g_eager[0], rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(m.qkv.bias.grad, g_eager[1], rtol=1e-5, atol=1e-5)
