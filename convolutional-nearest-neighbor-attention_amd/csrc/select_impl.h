@@ -26,15 +26,16 @@
 //
 // Two passes over the candidates:
 //  1. per lane, the maximum of each 16-candidate group (4-candidate groups
-//     when Nq <= 512; for d >= 256 on rows of at least 64 tiles only the
-//     first quarter of the tiles is swept) goes into a sorted
+//     when Nq <= 512; rows of more than 16 tiles sweep only their first half,
+//     their first quarter for d >= 256 and at least 64 tiles) goes into a sorted
 //     register list (med3 insertion); the K-th largest of the union of both
 //     half-lanes' lists is a lower bound tau of the token's K-th key, because
 //     it is attained by K distinct candidates.
 //  2. the tiles are recomputed and every key >= tau is appended to a per-lane
 //     LDS queue (about K + few entries per token).  When a queue fills, and at
-//     the end, the lower half-lane merges both half-lanes' queues into the
-//     token's one sorted (key, index) list in LDS; tau then rises to just
+//     the end, each half-lane sorts its queue into a list and the lower half
+//     merges the two into the token's one sorted (key, index) list in LDS
+//     (a bitonic top-K merge); tau then rises to just
 //     above the list's K-th key for both halves.  Drains happen at tile
 //     positions where both halves have consumed a prefix of the candidate
 //     indices, so a later candidate never ties its way in ahead of a listed
@@ -361,12 +362,12 @@ void select_kernel(SelArgs a) {
     // tau is the exact K-th key and only about K candidates reach the queues.
     const bool every = KMAX >= 16 && ntiles <= 8;
     const bool fine = ntiles <= 16;
-    // Wide heads on long rows (d >= 256, at least 64 tiles: config 5) draw the
-    // bound from the first quarter of the tiles: any candidates give a valid
-    // bound, and there one sweep costs more than the extra passers it lets
-    // through (c5 select 598 -> 521 us; at d = 128 the extra passers cost more
-    // than the sweep saves, and the whole row is used).
-    const int p1 = (NCH * Mfma<T>::KC >= 256 && ntiles >= 64) ? (ntiles + 3) / 4 : ntiles;
+    // Long rows draw the bound from the first half of the tiles (the first
+    // quarter for d >= 256 on rows of at least 64 tiles, config 5): any
+    // candidates give a valid bound, and there a pass-1 sweep costs more than
+    // the extra passers it lets through (c3 select 93 -> 89 us, c5 527 -> 490).
+    const int p1 = (NCH * Mfma<T>::KC >= 256 && ntiles >= 64) ? (ntiles + 3) / 4
+                                                              : (ntiles > 16 ? (ntiles + 1) / 2 : ntiles);
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) L[r] = -INFINITY;
     // MASKED: the tile runs past Nq (only the last one); its extra rows drop out
@@ -419,26 +420,47 @@ void select_kernel(SelArgs a) {
     uint16_t* myqi = qidx + tid;
     int woff = 0;   // cnt * NT: offset of this lane's next queue slot
     // both half-lanes' queues go into the token's list; only the lower half works
+    // Each half-lane inserts its own queue into a list (the lower half starts
+    // from the token's stored list, the upper half from an empty one); the
+    // lower half then takes the top K of both lists with a bitonic merge:
+    // M[r] = max(A[r], B[KP-1-r]) of two descending lists is a bitonic
+    // sequence holding the KP largest, which a half-cleaner network sorts.
     auto drain = [&]() __attribute__((always_inline)) {
       const int cnt = (int)((unsigned)woff / NT);
-      const int cntp = __shfl_xor(cnt, 32);
       float ntau = tau;
-      if (half == 0) {
-        uint64_t L2[KMAX];
+      uint64_t L2[KMAX];
 #pragma unroll
-        for (int r = 0; r < KMAX; ++r) L2[r] = lst[r * TPB + slot];
-        const int n = cnt > cntp ? cnt : cntp;
-        for (int e = 0; __any(e < n); ++e) {
-          // lanes past a count insert 0, which never moves the list
-          const uint64_t x0 = (e < cnt) ? pack_entry(__uint_as_float(myq[e * NT]), myqi[e * NT]) : 0;
-          const uint64_t x1 =
-              (e < cntp) ? pack_entry(__uint_as_float(myq[e * NT + 32]), myqi[e * NT + 32]) : 0;
-          list_insert<KMAX>(L2, x0);
-          list_insert<KMAX>(L2, x1);
+      for (int r = 0; r < KMAX; ++r) L2[r] = half == 0 ? lst[r * TPB + slot] : 0;
+      for (int e = 0; __any(e < cnt); ++e) {
+        const uint64_t x = (e < cnt) ? pack_entry(__uint_as_float(myq[e * NT]), myqi[e * NT]) : 0;
+        list_insert<KMAX>(L2, x);
+      }
+      constexpr int KP = KMAX <= 8 ? 8 : (KMAX <= 16 ? 16 : 32);
+      uint64_t M[KP];
+#pragma unroll
+      for (int r = 0; r < KP; ++r) {
+        const int rp = KP - 1 - r;
+        uint64_t p = 0;
+        if (rp < KMAX) {
+          const uint32_t lo = __shfl_xor((uint32_t)L2[rp], 32), hi = __shfl_xor((uint32_t)(L2[rp] >> 32), 32);
+          p = ((uint64_t)hi << 32) | lo;
         }
+        const uint64_t m = r < KMAX ? L2[r] : 0;
+        M[r] = m > p ? m : p;
+      }
 #pragma unroll
-        for (int r = 0; r < KMAX; ++r) lst[r * TPB + slot] = L2[r];
-        const uint64_t kth = pick<KMAX>(L2, a.Ksel - 1);
+      for (int j = KP / 2; j >= 1; j >>= 1)
+#pragma unroll
+        for (int i = 0; i < KP; ++i)
+          if ((i & j) == 0) {
+            const uint64_t u = M[i], v = M[i + j];
+            M[i] = u > v ? u : v;
+            M[i + j] = u > v ? v : u;
+          }
+      if (half == 0) {
+#pragma unroll
+        for (int r = 0; r < KMAX; ++r) lst[r * TPB + slot] = M[r];
+        const uint64_t kth = pick<KMAX>(reinterpret_cast<const uint64_t(&)[KMAX]>(M), a.Ksel - 1);
         if (kth != 0) ntau = fmaxf(ntau, next_up(key_of_ord((uint32_t)(kth >> 32))));
       }
       tau = __shfl(ntau, lane & 31);
