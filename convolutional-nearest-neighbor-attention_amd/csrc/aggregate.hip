@@ -254,11 +254,12 @@ __global__ __launch_bounds__(256, agg_min_blocks<KM>()) void agg_kernel(AggArgs 
   if (F0 % a.N == 0 && F1 % a.N == 0 && na % ZV == 0 && (h * dout + a_lo) % ZV == 0 && a.C % ZV == 0) {
     // the block covers na whole columns of Z, a multiple of ZV (16 aligned
     // bytes per row and group): a thread per (row t, column group) gathers the
-    // group from ZV staged rows, one 16-byte store
+    // group from ZV staged rows, one 16-byte store; the groups of a row are on
+    // adjacent lanes, so a row's segment is one contiguous write (c3: 30 -> 27 us)
     T* Zb = static_cast<T*>(a.out) + (int64_t)b * a.N * a.C + h * dout + a_lo;
     const int ng = na / ZV;
     for (int e = tid; e < a.N * ng; e += 256) {
-      const int gq = e / a.N, t = e - gq * a.N;
+      const int t = e / ng, gq = e - t * ng;
       union {
         u32x4_t u;
         T e[ZV];
