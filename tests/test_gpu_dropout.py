@@ -27,6 +27,7 @@ CASES = [
     # (dtype, H, dk, N, K, sampling, num_samples, conv, p)
     (torch.float32, 3, 32, 64, 9, "all", -1, "depthwise", 0.1),
     (torch.bfloat16, 3, 64, 197, 9, "all", -1, "depthwise", 0.1),
+    (torch.float16, 3, 64, 197, 9, "all", -1, "depthwise", 0.1),
     (torch.float32, 1, 24, 50, 5, "all", -1, "standard", 0.3),
     (torch.float32, 2, 16, 40, 6, "random", 20, "depthwise-separable", 0.2),
 ]

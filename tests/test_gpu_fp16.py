@@ -190,3 +190,28 @@ def test_kvt_fp16_matches_oracle_on_own_projections():
     z = o.view(B, H, N, dk).transpose(1, 2).reshape(B, N, C).to(H16).double()
     want = z @ m.proj.weight.detach().double().cpu().T
     torch.testing.assert_close(got.double().cpu(), want, rtol=5e-3, atol=5e-3)
+
+
+@pytest.mark.parametrize("topk,bias", [(9, True), (48, False)])
+def test_kvt_fp16_backward(topk, bias):
+    """float16 KVT training step (qkv_bias, and a selection wider than one
+    32-entry list) against oracle autograd in float64 (relative L2 1e-2)."""
+    torch.manual_seed(11)
+    C, H = 96, 3
+    m = MultiHeadKvtAttention(C, num_heads=H, topk=topk, qkv_bias=bias).to(DEV)
+    if bias:
+        with torch.no_grad():
+            m.qkv.bias.normal_(0, 0.5)
+    m = m.to(H16).train()
+    x = torch.randn(2, 197, C, device=DEV).to(H16).requires_grad_(True)
+    m(x).float().square().sum().backward()
+    xc = x.detach().double().cpu().requires_grad_(True)
+    Wqkv = m.qkv.weight.detach().double().cpu().requires_grad_(True)
+    bq = None if not bias else m.qkv.bias.detach().double().cpu().requires_grad_(True)
+    Wp = m.proj.weight.detach().double().cpu().requires_grad_(True)
+    O.kvt(xc, Wqkv, Wp, H, topk, m.scale, bqkv=bq).square().sum().backward()
+    pairs = [(x.grad, xc.grad), (m.qkv.weight.grad, Wqkv.grad), (m.proj.weight.grad, Wp.grad)]
+    if bias:
+        pairs.append((m.qkv.bias.grad, bq.grad))
+    for g, e in pairs:
+        assert rel_l2(g.cpu(), e) < 2e-2, rel_l2(g.cpu(), e)

@@ -34,6 +34,7 @@ CASES = [
     (16, 1024, 384, 3, 9, torch.bfloat16, "matmul", "depthwise", 1),
     (4, 512, 384, 3, 9, torch.bfloat16, "matmul", "depthwise", 2),
     (2, 197, 192, 3, 9, torch.float32, "cosine", "standard", 3),
+    (2, 150, 128, 2, 40, torch.float16, "matmul", "depthwise", 5),
     (1, 65, 96, 2, 5, torch.float32, "euclidean", "depthwise-separable", 4),
 ]
 
