@@ -534,6 +534,264 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
     }
 }
 
+// ---- Direct-to-LDS variant for 16-bit types with row-major A, Kd % 64 == 0,
+// 16-byte aligned rows and the staged epilogue (no LayerNorm prologue, no
+// statistics epilogue).  Tile 128 x 192 x 64, 4 waves of 64 x 96 (2 x 3 MFMA
+// blocks), two blocks per CU.  The operand tiles go from global memory straight
+// into LDS (global_load_lds_dwordx4: lane l of an instruction writes bytes
+// [16 l, 16 l + 16) after the wave-uniform base in M0), so one instruction
+// fills 8 rows of 128 bytes; a lane fetches the 16-byte chunk
+// (l % 8) ^ ((row / 2) % 8) of its row, so the MFMA operand reads (16 lanes =
+// 16 rows at one chunk) hit 16 distinct 16-byte slots of each 256-byte bank
+// window.  Two LDS stages: the loads of k-tile t + 1 are in flight while tile t
+// is multiplied.  Measured against the register-staged kernel at the workload
+// shapes: Q/K/V projection (M = 32768, N = 1152, K = 384) 41 vs 52 us, W_o
+// (N = K = 384) 15.6 vs 17.3 us.
+constexpr int DL_BM = 128, DL_BN = 192, DL_BK = 64;
+
+CNNA_DEV void load_to_lds16(const void* gp, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gp), "{m0}"(lds_base) : "memory");
+}
+
+template <typename T, int OMODE, int EPI>
+__global__ __launch_bounds__(256, 2) void gemm_dl_kernel(GemmArgs g) {
+  using M_ = Mfma<T>;
+  constexpr int MI = 2, NJ = 3, BM = DL_BM, BN = DL_BN, BK = DL_BK;
+  constexpr int ROWB = BK * (int)sizeof(T);   // 128-byte LDS rows, unpadded
+  constexpr int RPI = 1024 / ROWB;            // rows filled by one wave instruction
+  constexpr int STAGE = (BM + BN) * ROWB;
+  constexpr int CP = BN + 8;                  // staged output row pitch (elements)
+  constexpr int SMB = 2 * STAGE > BM * CP * (int)sizeof(T) ? 2 * STAGE : BM * CP * (int)sizeof(T);
+  constexpr int AI = BM / RPI / 4, WI = BN / RPI / 4;
+  static_assert(ROWB == 128 && BM % (RPI * 4) == 0 && BN % (RPI * 4) == 0, "tile shape");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[SMB];
+  const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int ncol = (g.Nc + BN - 1) / BN;
+  const int nrow = (g.M + BM - 1) / BM;
+  const int wid = xcd_swizzle(blockIdx.x, ncol * nrow);
+  const int n0 = (wid % ncol) * BN, m0 = (wid / ncol) * BM;
+  auto chunk = [](int row, int c) { return c ^ ((row >> 1) & 7); };
+
+  // sources of this lane's load instructions (rows clamped into range)
+  const T* A = static_cast<const T*>(g.a);
+  const T* asrc[AI];
+  const T* wsrc[WI];
+#pragma unroll
+  for (int i = 0; i < AI; ++i) {
+    const int r = (i * 4 + wave) * RPI + (lane >> 3);
+    const int m = min(m0 + r, g.M - 1);
+    int64_t sr = m;
+    if (g.arow != nullptr) {
+      const int b = m / g.a_rows, rr = m - b * g.a_rows;
+      sr = (int64_t)b * g.a_src_rows + g.arow[rr];
+    }
+    asrc[i] = A + sr * g.lda + chunk(r, lane & 7) * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < WI; ++i) {
+    const int r = (i * 4 + wave) * RPI + (lane >> 3);
+    const int n = min(n0 + r, g.Nc - 1);
+    const int mat = n / g.ncol_each;
+    wsrc[i] = static_cast<const T*>(g.w[mat]) + (int64_t)(n - mat * g.ncol_each) * g.Kd + chunk(r, lane & 7) * 8;
+  }
+  auto issue = [&](int buf, int k0) __attribute__((always_inline)) {
+    const uint32_t st = sbase + buf * STAGE;
+#pragma unroll
+    for (int i = 0; i < AI; ++i) load_to_lds16(asrc[i] + k0, st + (i * 4 + wave) * RPI * ROWB);
+#pragma unroll
+    for (int i = 0; i < WI; ++i) load_to_lds16(wsrc[i] + k0, st + (BM + (i * 4 + wave) * RPI) * ROWB);
+  };
+
+  f32x16_t acc[MI][NJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+  const int arow = wm * MI * 32 + (lane & 31), brow = wn * NJ * 32 + (lane & 31);
+  auto compute = [&](int buf) __attribute__((always_inline)) {
+    const unsigned char* sp = smem + buf * STAGE;
+#pragma unroll
+    for (int ks = 0; ks < BK / M_::KC; ++ks) {
+      const int cb = chunk(lane & 31, ks * 2 + (lane >> 5)) * 16;
+      typename M_::frag af[MI], bfr[NJ];
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+        af[i] = __builtin_bit_cast(typename M_::frag, *reinterpret_cast<const u32x4_t*>(sp + (arow + i * 32) * ROWB + cb));
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        bfr[j] = __builtin_bit_cast(typename M_::frag, *reinterpret_cast<const u32x4_t*>(sp + (BM + brow + j * 32) * ROWB + cb));
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc[i][j] = M_::mma(bfr[j], af[i], acc[i][j]);
+    }
+  };
+  const int nk = g.Kd / BK;
+  issue(0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's loads of tile kt are in LDS
+    __syncthreads();                      // ... everyone's; and tile kt - 1 is consumed
+    if (kt + 1 < nk) issue((kt + 1) & 1, (kt + 1) * BK);
+    compute(kt & 1);
+  }
+  __syncthreads();
+
+  // ---- epilogue: the tile is staged through LDS (bias / GELU applied on the
+  // way) and written back as 16-byte row segments
+  T* Cs = reinterpret_cast<T*>(smem);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    float bq[EPI ? 4 : 1][4];
+    if (EPI) {
+      const T* bp = static_cast<const T*>(g.bias);
+#pragma unroll
+      for (int vq = 0; vq < (EPI ? 4 : 1); ++vq) {
+        const int n = n0 + wn * NJ * 32 + j * 32 + vq * 8 + (lane >> 5) * 4;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) bq[vq][u] = bp != nullptr ? ldf(bp + min(n + u, g.Nc - 1)) : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int vq = 0; vq < 4; ++vq) {
+        const int ml = wm * MI * 32 + i * 32 + (lane & 31);
+        const int nl = wn * NJ * 32 + j * 32 + vq * 8 + (lane >> 5) * 4;
+        const f32x16_t& a = acc[i][j];
+        float e[4] = {a[vq * 4], a[vq * 4 + 1], a[vq * 4 + 2], a[vq * 4 + 3]};
+        if (EPI) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            float v = e[u] + bq[EPI ? vq : 0][u];
+            if (EPI == 2) v = gelu_erf(rnd_to(v, T(0)));   // rounded as nn.Linear's output
+            e[u] = v;
+          }
+        }
+        uint2 u;
+        u.x = Pair16<T>::pack(e[0], e[1]);
+        u.y = Pair16<T>::pack(e[2], e[3]);
+        *reinterpret_cast<uint2*>(&Cs[ml * CP + nl]) = u;
+      }
+  }
+  __syncthreads();
+  // 192 threads: thread -> fixed 8-column group, rows (tid / 24) + 8 * it, so
+  // the head-split coordinates are derived once and stepped
+  constexpr int SEGS = BN / 8;
+  if (tid >= SEGS * 8) return;
+  const int nl = (tid % SEGS) * 8;
+  const int n = n0 + nl;
+  if (n >= g.Nc) return;
+  int mat = 0, hh = 0, cc = n, b = 0, r = 0;
+  bool whole = n + 8 <= g.Nc;
+  const int mfirst = m0 + tid / SEGS;
+  if (OMODE == GEMM_O_HEADSPLIT) {
+    mat = n / g.ncol_each;
+    const int nn = n - mat * g.ncol_each;
+    hh = nn / g.o_dk;
+    cc = nn - hh * g.o_dk;
+    whole = whole && (cc + 8 <= g.o_dk);
+    b = mfirst / g.o_rows;
+    r = mfirst - b * g.o_rows;
+  }
+  T* obase = static_cast<T*>(g.o[OMODE == GEMM_O_HEADSPLIT ? (mat > 2 ? 2 : mat) : 0]);
+  // output offset of this thread's segment, stepped by 8 rows (recomputed when
+  // the head-split row wraps into the next sequence)
+  auto seg_off = [&](int m) -> int64_t {
+    return OMODE == GEMM_O_HEADSPLIT ? (((int64_t)b * g.o_H + hh) * g.o_rows + r) * g.o_dkp + cc
+                                     : (int64_t)m * g.ldo + n;
+  };
+  int64_t off = seg_off(mfirst);
+  const int64_t ostep = OMODE == GEMM_O_HEADSPLIT ? 8 * (int64_t)g.o_dkp : 8 * g.ldo;
+#pragma unroll
+  for (int it = 0; it < BM / 8; ++it) {
+    const int ml = tid / SEGS + it * 8;
+    const int m = m0 + ml;
+    if (it > 0) {
+      if (OMODE == GEMM_O_HEADSPLIT) {
+        r += 8;
+        if (r >= g.o_rows) {
+          b = m / g.o_rows;
+          r = m - b * g.o_rows;
+          off = seg_off(m);
+        } else {
+          off += ostep;
+        }
+      } else {
+        off += ostep;
+      }
+    }
+    if (m >= g.M) break;
+    u32x4_t val = *reinterpret_cast<const u32x4_t*>(&Cs[ml * CP + nl]);
+    if (EPI && g.res != nullptr && whole) {
+      // residual: 16-bit linear output + 16-bit residual, added in fp32 and rounded once
+      const u32x4_t rv = *reinterpret_cast<const u32x4_t*>(static_cast<const T*>(g.res) + (int64_t)m * g.ldr + n);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        val[q] = Pair16<T>::pack(Pair16<T>::lo(val[q]) + Pair16<T>::lo(rv[q]),
+                                 Pair16<T>::hi(val[q]) + Pair16<T>::hi(rv[q]));
+    }
+    T* dst = obase + off;
+    if (whole) {
+      *reinterpret_cast<u32x4_t*>(dst) = val;
+    } else {
+      // tile or head edge: element by element
+      for (int u = 0; u < 8 && n + u < g.Nc; ++u) {
+        const T v = Cs[ml * CP + nl + u];
+        if (OMODE == GEMM_O_HEADSPLIT) {
+          const int nu = n + u;
+          const int mt = nu / g.ncol_each, nn = nu - mt * g.ncol_each;
+          const int h = nn / g.o_dk, c = nn - h * g.o_dk;
+          static_cast<T*>(g.o[mt])[(((int64_t)b * g.o_H + h) * g.o_rows + r) * g.o_dkp + c] = v;
+        } else {
+          if (EPI && g.res != nullptr)
+            stf(&dst[u], ldf(&v) + ldf(static_cast<const T*>(g.res) + (int64_t)m * g.ldr + n + u));
+          else
+            dst[u] = v;
+        }
+      }
+    }
+  }
+}
+
+// the direct-to-LDS kernel for the linear GEMMs it covers; DL_SKIP when the
+// call is not one of them
+constexpr int DL_SKIP = 0x7fffffff;
+template <typename T>
+int launch_dl(int amode, int omode, const GemmArgs& g, hipStream_t s) {
+  if constexpr (sizeof(T) != 2) {
+    return DL_SKIP;
+  } else {
+    if (amode != GEMM_A_ROWS || !g.ostage || g.ln_stats || g.st_out) return DL_SKIP;
+    if (!g.avec || !g.bvec || g.Kd % DL_BK != 0) return DL_SKIP;
+    // 16-byte aligned sources for every row (the loads bypass the registers)
+    if ((uintptr_t)g.a % 16 != 0 || (g.lda * (int64_t)sizeof(T)) % 16 != 0) return DL_SKIP;
+    for (int i = 0; i < 3; ++i)
+      if (g.w[i] && (uintptr_t)g.w[i] % 16 != 0) return DL_SKIP;
+    const dim3 grid(((g.Nc + DL_BN - 1) / DL_BN) * ((g.M + DL_BM - 1) / DL_BM));
+    const bool gelu = g.act == GEMM_ACT_GELU;
+    if (omode == GEMM_O_HEADSPLIT) {
+      if (g.res || gelu) return CNNA_ERR_OPTION;
+      if (g.bias)
+        hipLaunchKernelGGL((gemm_dl_kernel<T, GEMM_O_HEADSPLIT, 1>), grid, dim3(256), 0, s, g);
+      else
+        hipLaunchKernelGGL((gemm_dl_kernel<T, GEMM_O_HEADSPLIT, 0>), grid, dim3(256), 0, s, g);
+    } else if (gelu) {
+      hipLaunchKernelGGL((gemm_dl_kernel<T, GEMM_O_PLAIN, 2>), grid, dim3(256), 0, s, g);
+    } else if (g.bias || g.res) {
+      hipLaunchKernelGGL((gemm_dl_kernel<T, GEMM_O_PLAIN, 1>), grid, dim3(256), 0, s, g);
+    } else {
+      hipLaunchKernelGGL((gemm_dl_kernel<T, GEMM_O_PLAIN, 0>), grid, dim3(256), 0, s, g);
+    }
+    return (int)hipGetLastError();
+  }
+}
+
 template <typename T, bool FAST>
 int launch_x(int omode, const GemmArgs& g, hipStream_t s, dim3 grid) {
   // LayerNorm prologue and / or statistics epilogue (row-major A)
@@ -619,6 +877,8 @@ int launch_t(int amode, int omode, const GemmArgs& g0, hipStream_t s) {
   if (g.res != nullptr) ostage = ostage && ((uintptr_t)g.res % 16 == 0) && (g.ldr % 8 == 0);
   else ostage = ostage && (g.o_dkp % 8 == 0) && (g.ncol_each % 8 == 0) && (g.o_dk % 8 == 0);
   g.ostage = ostage;
+  const int dl = launch_dl<T>(amode, omode, g, s);
+  if (dl != DL_SKIP) return dl;
   const bool fast = g.avec && g.bvec && (g.Kd % GemmCfg<T>::BK == 0);
   return fast ? launch_f<T, true>(amode, omode, g, s) : launch_f<T, false>(amode, omode, g, s);
 }

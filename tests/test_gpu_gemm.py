@@ -66,3 +66,20 @@ def test_staged_tiles_exact_selection():
     torch.cuda.synchronize()
     ref = a.float()[:, torch.arange(N, device=DEV) % K]
     assert torch.equal(out.float(), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", [(128 * 33 + 5, 192 * 5 + 8, 192), (4099, 384, 384), (1000, 200, 64)])
+def test_direct_tiles_exact_selection(dtype, M, N, K):
+    """The 16-bit row GEMM loads its operand tiles straight into LDS with the
+    16-byte chunks of each row permuted.  A ramp A against a 0/1 selection W
+    (column n picks A column (7 n + 3) % K) makes every output one exact A
+    element, so a misplaced chunk, row or k-tile shows up as a wrong value;
+    partial row and column tiles are included."""
+    a = (torch.arange(M * K, device=DEV) % 251).view(M, K).to(dtype)
+    pick = (torch.arange(N, device=DEV) * 7 + 3) % K
+    W = torch.zeros(N, K, device=DEV)
+    W[torch.arange(N, device=DEV), pick] = 1.0
+    out = ops.linear(a, W.to(dtype))
+    torch.cuda.synchronize()
+    assert torch.equal(out.float(), a.float()[:, pick])
