@@ -55,8 +55,8 @@ TRAIN = {"c5"}
 STAGE_KERNELS = {  # bench stage -> substring of the HIP kernel name
     "select": "select_kernel",
     "aggregate": "agg_kernel",
-    "project": "gemm_kernel<unsigned short, 0, 1",
-    "output_proj": "gemm_kernel<unsigned short, 0, 0",
+    "project": "gemm_dl_kernel<unsigned short, 1",
+    "output_proj": "gemm_dl_kernel<unsigned short, 0",
 }
 
 
