@@ -34,9 +34,9 @@ const char* cnna_error_string(int code) {
              "cnna_forward_noalloc; call cnna_forward with a workspace";
     case CNNA_ERR_UNSUPPORTED:
       return "cnna: configuration not supported by this build (limits: K <= 64 neighbours in the "
-             "backward, head width d_k (+1 with coordinate encoding) <= 256 for 16-bit types and <= 128 for "
-             "float32, at most 65536 candidates; folded LayerNorm: C <= 1024; row statistics "
-             "epilogue: bfloat16, Nout % 8 == 0, 16-byte aligned out / res with row strides that "
+             "backward, head width d_k (+1 with coordinate encoding) <= 256, at most 65536 "
+             "candidates; folded LayerNorm: C <= 1024; row statistics "
+             "epilogue: 16-bit types, Nout % 8 == 0, 16-byte aligned out / res with row strides that "
              "are multiples of 8 elements)";
     default: break;
   }
@@ -59,8 +59,7 @@ int cnna_check_desc(const cnna_desc* d) {
   if (d->merge == CNNA_MERGE_REFERENCE && d->H > 1 && d->seq_length != d->N) return CNNA_ERR_SEQ_LENGTH;
   // the reference accepts these; the kernels' tiles do not
   const int dkp = dkp_of(d);
-  if (d->dtype != CNNA_F32 && dkp > 256) return CNNA_ERR_UNSUPPORTED;
-  if (d->dtype == CNNA_F32 && dkp > 128) return CNNA_ERR_UNSUPPORTED;
+  if (dkp > 256) return CNNA_ERR_UNSUPPORTED;
   if (d->Nq > 65536) return CNNA_ERR_UNSUPPORTED;
   return CNNA_OK;
 }

@@ -63,9 +63,11 @@ constexpr int QCHK = 4;     // elements between queue checks
 constexpr int NT = 256;     // threads per block
 
 template <typename T> struct SelCfg;
-template <> struct SelCfg<uint16_t> { static constexpr int MAXCH = 16, VEC = 8; };  // d <= 256
-template <> struct SelCfg<_Float16> { static constexpr int MAXCH = 16, VEC = 8; };  // d <= 256
-template <> struct SelCfg<float> { static constexpr int MAXCH = 64, VEC = 4; };     // d <= 128
+// MAXCH: chunks of the regular instances; WIDECH: chunks of the wide-head
+// instances (key rows of 128 registers per lane, one block per CU)
+template <> struct SelCfg<uint16_t> { static constexpr int MAXCH = 16, WIDECH = 16, VEC = 8; };  // d <= 256
+template <> struct SelCfg<_Float16> { static constexpr int MAXCH = 16, WIDECH = 16, VEC = 8; };  // d <= 256
+template <> struct SelCfg<float> { static constexpr int MAXCH = 64, WIDECH = 128, VEC = 4; };    // d <= 128, wide 256
 
 // A (key, index) pair as one 64-bit integer ordered like the ranking (larger
 // key first, then lower index): high word = order-preserving image of the float key, low word = ~index.
@@ -642,8 +644,10 @@ __global__ __launch_bounds__(256) void sel_weights_kernel(const float* vals, flo
 // one list of KMAX entries, or rounds of 32 for wider selections
 template <typename T, int NCH, bool EXACT, bool EUC>
 int launch_rounds(int sampled, const SelArgs& a, hipStream_t s) {
-  if (EXACT && a.Ksel <= 9) return launch_k<T, NCH, EXACT, 9, EUC>(sampled, a, s);
-  if (EXACT && a.Ksel <= 16) return launch_k<T, NCH, EXACT, 16, EUC>(sampled, a, s);
+  if constexpr (EXACT) {
+    if (a.Ksel <= 9) return launch_k<T, NCH, EXACT, 9, EUC>(sampled, a, s);
+    if (a.Ksel <= 16) return launch_k<T, NCH, EXACT, 16, EUC>(sampled, a, s);
+  }
   if (a.Ksel <= 32) return launch_k<T, NCH, EXACT, 32, EUC>(sampled, a, s);
   SelArgs r = a;
   r.w = nullptr;
@@ -669,7 +673,7 @@ int launch_n(int sampled, const SelArgs& a, hipStream_t s) {
 
 template <typename T, bool EUC>
 int launch_select_t(int sampled, const SelArgs& a, hipStream_t s) {
-  if (a.dkp % Mfma<T>::KC != 0 || a.dkp > SelCfg<T>::MAXCH * Mfma<T>::KC || a.dkp % SelCfg<T>::VEC != 0)
+  if (a.dkp % Mfma<T>::KC != 0 || a.dkp > SelCfg<T>::WIDECH * Mfma<T>::KC || a.dkp % SelCfg<T>::VEC != 0)
     return CNNA_ERR_SHAPE;
   if (a.Nq > 65536) return CNNA_ERR_SHAPE;
   // the queue region also stages one output array (TPB * K <= TPB * 32 values) at the end
@@ -680,6 +684,11 @@ int launch_select_t(int sampled, const SelArgs& a, hipStream_t s) {
   if (nch == q) return launch_n<T, q, EUC>(sampled, a, s);
   if (nch == 2 * q) return launch_n<T, 2 * q, EUC>(sampled, a, s);
   if (nch == 4 * q) return launch_n<T, 4 * q, EUC>(sampled, a, s);
+  if constexpr (SelCfg<T>::WIDECH > SelCfg<T>::MAXCH) {
+    // float32 heads wider than 128: 256 exactly, or guarded chunks up to 256
+    if (nch == SelCfg<T>::WIDECH) return launch_n<T, SelCfg<T>::WIDECH, EUC>(sampled, a, s);
+    if (nch > SelCfg<T>::MAXCH) return launch_rounds<T, SelCfg<T>::WIDECH, false, EUC>(sampled, a, s);
+  }
   // other widths: guarded chunks, lists of 32
   return launch_rounds<T, SelCfg<T>::MAXCH, false, EUC>(sampled, a, s);
 }

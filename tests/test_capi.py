@@ -65,7 +65,8 @@ def test_check_desc_ok():
     (dict(K=0), ops.ERR_K_RANGE),
     # valid for the reference, beyond the kernels' limits: NotImplementedError, not a range error
     (dict(C=3 * 264, dtype=ops.CNNA_BF16), ops.ERR_UNSUPPORTED),   # bf16 head width > 256
-    (dict(C=3 * 136), ops.ERR_UNSUPPORTED),                        # f32 head width > 128
+    (dict(C=3 * 264), ops.ERR_UNSUPPORTED),                        # f32 head width > 256
+    (dict(C=2 * 256, H=2, conv=0, coord=1), ops.ERR_UNSUPPORTED),  # 256 + coordinate channel
     (dict(N=70000, Nq=70000, seq_length=70000), ops.ERR_UNSUPPORTED),
 ])
 def test_check_desc_errors(kw, code):
@@ -199,3 +200,10 @@ def test_wide_k_forward_accepted_backward_limited():
                                     ctypes.byref(sv), fake, ctypes.byref(gr), fake, 1 << 30, None)
     assert st == ops.ERR_UNSUPPORTED
     assert b"K <= 64" in ops.LIB.cnna_error_string(ops.ERR_UNSUPPORTED)
+
+
+def test_wide_float32_heads_accepted():
+    # float32 heads up to 256 channels (the wide select instances), as for 16-bit types
+    assert status(C=2 * 256, H=2) == 0
+    assert status(C=2 * 192, H=2) == 0
+    assert status(C=2 * 255, H=2, conv=0, coord=1) == 0

@@ -117,6 +117,12 @@ SELECT_CASES = [
     ("random_matmul_f32", dict(d_hidden=192, num_heads=3, K=9, sampling_type="random", num_samples=64, seq_length=197), 4, 197, torch.float32),
     ("spatial_cosine_f32", dict(d_hidden=192, num_heads=3, K=9, sampling_type="spatial", num_samples=8, magnitude_type="cosine", seq_length=197), 4, 197, torch.float32),
     ("random_euclid_f32", dict(d_hidden=64, num_heads=2, K=6, sampling_type="random", num_samples=20, magnitude_type="euclidean", seq_length=70), 2, 70, torch.float32),
+    # float32 heads wider than 128 (key rows of 128 registers, one block per CU):
+    # d_k = 256 exactly, and guarded chunks for d_k = 192 / 200
+    ("d256_f32", dict(d_hidden=512, num_heads=2, K=9, seq_length=300), 2, 300, torch.float32),
+    ("d256_k16_random_euclid_f32", dict(d_hidden=768, num_heads=3, K=16, sampling_type="random", num_samples=100, magnitude_type="euclidean", seq_length=197), 2, 197, torch.float32),
+    ("d192_cosine_f32", dict(d_hidden=384, num_heads=2, K=9, magnitude_type="cosine", seq_length=150), 2, 150, torch.float32),
+    ("d200_k40_f32", dict(d_hidden=400, num_heads=2, K=40, seq_length=120), 2, 120, torch.float32),
 ]
 
 
@@ -192,6 +198,10 @@ E2E_CASES = [
     ("spatial_pad_euclid_raw", dict(d_hidden=48, num_heads=3, K=4, sampling_type="spatial", num_samples=6, sample_padding=2, magnitude_type="euclidean", softmax_topk_val=False, seq_length=30), 2, 30),
     ("coord_std_random", dict(d_hidden=64, num_heads=2, K=5, sampling_type="random", num_samples=12, coordinate_encoding=True, convolution_type="standard", seq_length=40), 2, 40),
     ("h1", dict(d_hidden=48, num_heads=1, K=7, seq_length=197), 2, 60),
+    # float32 heads wider than 128
+    ("d256_dw_f32", dict(d_hidden=512, num_heads=2, K=9, seq_length=120), 2, 120),
+    ("d256_std_k16_f32", dict(d_hidden=768, num_heads=3, K=16, convolution_type="standard", seq_length=100), 1, 100),
+    ("d192_coord_std_random_f32", dict(d_hidden=384, num_heads=2, K=5, sampling_type="random", num_samples=40, coordinate_encoding=True, convolution_type="standard", seq_length=60), 2, 60),
 ]
 
 
