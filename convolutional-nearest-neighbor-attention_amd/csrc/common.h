@@ -145,6 +145,22 @@ CNNA_DEV float gelu_erf(float x) {
   return 0.5f * x * (x >= 0.0f ? 2.0f - erfc : erfc);
 }
 
+// The value of lane l ^ 32 (the other half of the wave) without a trip through
+// LDS: v_permlane32_swap exchanges lanes 32..63 of its first operand with lanes
+// 0..31 of its second; with both operands x, the lower half finds the upper
+// half's values in the second result and the upper half the lower half's in
+// the first.
+CNNA_DEV uint32_t xor32(uint32_t x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return __lane_id() < 32 ? r[1] : r[0];
+}
+CNNA_DEV float xor32(float x) { return __uint_as_float(xor32(__float_as_uint(x))); }
+// lanes 32..63 take the value of lane l - 32, lanes 0..31 keep their own
+CNNA_DEV float from_lower(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __lane_id() < 32 ? x : __uint_as_float(r[0]);
+}
+
 // Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), every lane gets
 // it; no LDS traffic.  All 16 lanes must be active.
 template <int CTRL>

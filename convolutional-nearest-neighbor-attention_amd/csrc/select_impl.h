@@ -410,7 +410,7 @@ void select_kernel(SelArgs a) {
     {
       float P[KMAX];
 #pragma unroll
-      for (int r = 0; r < KMAX; ++r) P[r] = __shfl_xor(L[r], 32);
+      for (int r = 0; r < KMAX; ++r) P[r] = xor32(L[r]);
 #pragma unroll
       for (int r = 0; r < KMAX; ++r) bound_insert<KMAX>(L, P[r]);
     }
@@ -444,7 +444,7 @@ void select_kernel(SelArgs a) {
         const int rp = KP - 1 - r;
         uint64_t p = 0;
         if (rp < KMAX) {
-          const uint32_t lo = __shfl_xor((uint32_t)L2[rp], 32), hi = __shfl_xor((uint32_t)(L2[rp] >> 32), 32);
+          const uint32_t lo = xor32((uint32_t)L2[rp]), hi = xor32((uint32_t)(L2[rp] >> 32));
           p = ((uint64_t)hi << 32) | lo;
         }
         const uint64_t m = r < KMAX ? L2[r] : 0;
@@ -465,7 +465,7 @@ void select_kernel(SelArgs a) {
         const uint64_t kth = pick<KMAX>(reinterpret_cast<const uint64_t(&)[KMAX]>(M), a.Ksel - 1);
         if (kth != 0) ntau = fmaxf(ntau, next_up(key_of_ord((uint32_t)(kth >> 32))));
       }
-      tau = __shfl(ntau, lane & 31);
+      tau = from_lower(ntau);
       woff = 0;
     };
     // Drains are synchronised across the block: a wave that would otherwise
