@@ -192,7 +192,7 @@ void select_kernel(SelArgs a) {
   int* cdt = reinterpret_cast<int*>(qnt + 2 * TJ);
   constexpr int QC = queue_cap<T, NCH, EXACT, KMAX, EUC, SMP>();
   // queue: key bits [QC][NT] (32-bit) followed by candidate indices [QC][NT]
-  // (16-bit), element woff of lane tid at qent[woff + tid] / qidx[woff + tid]
+  // (16-bit); slot e of lane tid at qent[e * NT + tid] / qidx[e * NT + tid]
   int* dflag = cdt + 2 * TJ;   // [2][4] per-wave drain requests, by tile parity
   uint32_t* qent = reinterpret_cast<uint32_t*>(dflag + 8);
 
@@ -420,7 +420,10 @@ void select_kernel(SelArgs a) {
 
     uint32_t* myq = qent + tid;
     uint16_t* myqi = qidx + tid;
-    int woff = 0;   // cnt * NT: offset of this lane's next queue slot
+    // this lane's next free queue slot, as running LDS pointers (an append is
+    // two stores and two pointer increments; no address arithmetic per value)
+    uint32_t* qk = myq;
+    uint16_t* qi = myqi;
     // both half-lanes' queues go into the token's list; only the lower half works
     // Each half-lane inserts its own queue into a list (the lower half starts
     // from the token's stored list, the upper half from an empty one); the
@@ -428,7 +431,7 @@ void select_kernel(SelArgs a) {
     // M[r] = max(A[r], B[KP-1-r]) of two descending lists is a bitonic
     // sequence holding the KP largest, which a half-cleaner network sorts.
     auto drain = [&]() __attribute__((always_inline)) {
-      const int cnt = (int)((unsigned)woff / NT);
+      const int cnt = (int)((qk - myq) / NT);
       float ntau = tau;
       uint64_t L2[KMAX];
 #pragma unroll
@@ -466,7 +469,8 @@ void select_kernel(SelArgs a) {
         if (kth != 0) ntau = fmaxf(ntau, next_up(key_of_ord((uint32_t)(kth >> 32))));
       }
       tau = from_lower(ntau);
-      woff = 0;
+      qk = myq;
+      qi = myqi;
     };
     // Drains are synchronised across the block: a wave that would otherwise
     // drain on its own mid-tile stalls the other waves at the next barrier, so
@@ -480,11 +484,13 @@ void select_kernel(SelArgs a) {
         const int* f = dflag + ((t - 1) & 1) * 4;
         if (__any((f[0] | f[1] | f[2] | f[3]) != 0)) drain();
       }
+      // candidate index of value v of MFMA block b: jt + b*32 + (v/4)*8 + v%4
+      const int jt = j0 + 4 * half;
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          if (v % QCHK == 0 && __any(woff > (QC - QCHK) * NT)) drain();
+          if (v % QCHK == 0 && __any(qk > myq + (QC - QCHK) * NT)) drain();
           const int jl = b * 32 + mfma_row(v, lane);
           float key = keyof(acc[b][v], buf, jl);
           if (decltype(MASKED)::value && j0 + jl >= a.Nq) key = __builtin_nanf("");
@@ -494,19 +500,22 @@ void select_kernel(SelArgs a) {
           if (PRED_APPEND) {
             // store the passers only; element steps where no lane passes skip it
             if (key >= tau) {
-              myq[woff] = __float_as_uint(key);
-              myqi[woff] = (uint16_t)(j0 + jl);
-              woff += NT;
+              *qk = __float_as_uint(key);
+              *qi = (uint16_t)(jt + (b * 32 + (v >> 2) * 8 + (v & 3)));
+              qk += NT;
+              qi += NT;
             }
           } else {
             // branch-free: write at the current slot, keep it only if it passed
-            myq[woff] = __float_as_uint(key);
-            myqi[woff] = (uint16_t)(j0 + jl);
-            woff += (key >= tau) ? NT : 0;
+            *qk = __float_as_uint(key);
+            *qi = (uint16_t)(jt + (b * 32 + (v >> 2) * 8 + (v & 3)));
+            const int adv = (key >= tau) ? NT : 0;
+            qk += adv;
+            qi += adv;
           }
         }
       }
-      const bool need = __any(woff > BTHR * NT);
+      const bool need = __any(qk > myq + BTHR * NT);
       if (lane == 0) dflag[(t & 1) * 4 + wave] = need ? 1 : 0;
     };
     sweep([&](const f32x16_t (&acc)[NB], int buf, int j0) __attribute__((always_inline)) {
