@@ -420,10 +420,14 @@ void select_kernel(SelArgs a) {
 
     uint32_t* myq = qent + tid;
     uint16_t* myqi = qidx + tid;
-    // this lane's next free queue slot, as running LDS pointers (an append is
-    // two stores and two pointer increments; no address arithmetic per value)
-    uint32_t* qk = myq;
-    uint16_t* qi = myqi;
+    // this lane's last written queue slot (one slot before the queue when it
+    // is empty), as running LDS pointers: an append is two increments and two
+    // stores at the new addresses, no address arithmetic per value
+    typedef __attribute__((address_space(3))) uint32_t lds_u32;
+    typedef __attribute__((address_space(3))) uint16_t lds_u16;
+    lds_u32* const qk0 = (lds_u32*)myq;
+    lds_u32* qk = qk0 - NT;
+    lds_u16* qi = (lds_u16*)myqi - NT;
     // both half-lanes' queues go into the token's list; only the lower half works
     // Each half-lane inserts its own queue into a list (the lower half starts
     // from the token's stored list, the upper half from an empty one); the
@@ -431,7 +435,7 @@ void select_kernel(SelArgs a) {
     // M[r] = max(A[r], B[KP-1-r]) of two descending lists is a bitonic
     // sequence holding the KP largest, which a half-cleaner network sorts.
     auto drain = [&]() __attribute__((always_inline)) {
-      const int cnt = (int)((qk - myq) / NT);
+      const int cnt = (int)((qk - qk0) / NT) + 1;
       float ntau = tau;
       uint64_t L2[KMAX];
 #pragma unroll
@@ -469,8 +473,8 @@ void select_kernel(SelArgs a) {
         if (kth != 0) ntau = fmaxf(ntau, next_up(key_of_ord((uint32_t)(kth >> 32))));
       }
       tau = from_lower(ntau);
-      qk = myq;
-      qi = myqi;
+      qk = qk0 - NT;
+      qi = (lds_u16*)myqi - NT;
     };
     // Drains are synchronised across the block: a wave that would otherwise
     // drain on its own mid-tile stalls the other waves at the next barrier, so
@@ -490,7 +494,7 @@ void select_kernel(SelArgs a) {
       for (int b = 0; b < NB; ++b) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          if (v % QCHK == 0 && __any(qk > myq + (QC - QCHK) * NT)) drain();
+          if (v % QCHK == 0 && __any(qk >= qk0 + (QC - QCHK) * NT)) drain();
           const int jl = b * 32 + mfma_row(v, lane);
           float key = keyof(acc[b][v], buf, jl);
           if (decltype(MASKED)::value && j0 + jl >= a.Nq) key = __builtin_nanf("");
@@ -500,22 +504,25 @@ void select_kernel(SelArgs a) {
           if (PRED_APPEND) {
             // store the passers only; element steps where no lane passes skip it
             if (key >= tau) {
-              *qk = __float_as_uint(key);
-              *qi = (uint16_t)(jt + (b * 32 + (v >> 2) * 8 + (v & 3)));
               qk += NT;
               qi += NT;
+              // keep the stores on the incremented registers (an add folded
+              // into the store offset would leave two live copies to merge)
+              asm volatile("" : "+v"(qk), "+v"(qi));
+              *qk = __float_as_uint(key);
+              *qi = (uint16_t)(jt + (b * 32 + (v >> 2) * 8 + (v & 3)));
             }
           } else {
             // branch-free: write at the current slot, keep it only if it passed
-            *qk = __float_as_uint(key);
-            *qi = (uint16_t)(jt + (b * 32 + (v >> 2) * 8 + (v & 3)));
+            qk[NT] = __float_as_uint(key);
+            qi[NT] = (uint16_t)(jt + (b * 32 + (v >> 2) * 8 + (v & 3)));
             const int adv = (key >= tau) ? NT : 0;
             qk += adv;
             qi += adv;
           }
         }
       }
-      const bool need = __any(qk > myq + BTHR * NT);
+      const bool need = __any(qk >= qk0 + BTHR * NT);
       if (lane == 0) dflag[(t & 1) * 4 + wave] = need ? 1 : 0;
     };
     sweep([&](const f32x16_t (&acc)[NB], int buf, int j0) __attribute__((always_inline)) {
