@@ -440,9 +440,41 @@ void select_kernel(SelArgs a) {
       uint64_t L2[KMAX];
 #pragma unroll
       for (int r = 0; r < KMAX; ++r) L2[r] = half == 0 ? lst[r * TPB + slot] : 0;
-      for (int e = 0; __any(e < cnt); ++e) {
-        const uint64_t x = (e < cnt) ? pack_entry(__uint_as_float(myq[e * NT]), myqi[e * NT]) : 0;
-        list_insert<KMAX>(L2, x);
+      if constexpr (RAW && !EX) {
+        // Raw dot-product keys are finite, so the list can hold float keys
+        // (-inf marks an empty slot) kept in order by one med3 per slot, and
+        // the indices follow the strict comparisons: a lane's queue holds its
+        // candidates in increasing index order and the stored list only earlier
+        // candidates, so a later equal key goes after the listed ones, which
+        // is the lowest-index-first order.  Packed again for the merge.
+        float Lk[KMAX];
+        uint32_t Li[KMAX];
+#pragma unroll
+        for (int r = 0; r < KMAX; ++r) {
+          Lk[r] = L2[r] == 0 ? -INFINITY : key_of_ord((uint32_t)(L2[r] >> 32));
+          Li[r] = ~(uint32_t)L2[r];
+        }
+        for (int e = 0; __any(e < cnt); ++e) {
+          const float xk = (e < cnt) ? __uint_as_float(myq[e * NT]) : -INFINITY;
+          const uint32_t xi = myqi[e * NT];
+          bool b[KMAX];
+#pragma unroll
+          for (int r = 0; r < KMAX; ++r) b[r] = xk > Lk[r];
+#pragma unroll
+          for (int r = KMAX - 1; r >= 1; --r) {
+            Lk[r] = __builtin_amdgcn_fmed3f(Lk[r - 1], xk, Lk[r]);
+            Li[r] = b[r - 1] ? Li[r - 1] : (b[r] ? xi : Li[r]);
+          }
+          Lk[0] = b[0] ? xk : Lk[0];
+          Li[0] = b[0] ? xi : Li[0];
+        }
+#pragma unroll
+        for (int r = 0; r < KMAX; ++r) L2[r] = Lk[r] == -INFINITY ? 0 : pack_entry(Lk[r], Li[r]);
+      } else {
+        for (int e = 0; __any(e < cnt); ++e) {
+          const uint64_t x = (e < cnt) ? pack_entry(__uint_as_float(myq[e * NT]), myqi[e * NT]) : 0;
+          list_insert<KMAX>(L2, x);
+        }
       }
       constexpr int KP = KMAX <= 8 ? 8 : (KMAX <= 16 ? 16 : 32);
       uint64_t M[KP];
