@@ -26,8 +26,8 @@
 //
 // Two passes over the candidates:
 //  1. per lane, the maximum of each 16-candidate group (4-candidate groups
-//     when Nq <= 512; rows of more than 16 tiles sweep only their first half,
-//     their first quarter for d >= 256 and at least 64 tiles) goes into a sorted
+//     when Nq <= 512; rows of more than 16 tiles sweep only their first three
+//     quarters, their first quarter for d >= 256 and at least 64 tiles) goes into a sorted
 //     register list (med3 insertion); the K-th largest of the union of both
 //     half-lanes' lists is a lower bound tau of the token's K-th key, because
 //     it is attained by K distinct candidates.
@@ -364,12 +364,14 @@ void select_kernel(SelArgs a) {
     // tau is the exact K-th key and only about K candidates reach the queues.
     const bool every = KMAX >= 16 && ntiles <= 8;
     const bool fine = ntiles <= 16;
-    // Long rows draw the bound from the first half of the tiles (the first
-    // quarter for d >= 256 on rows of at least 64 tiles, config 5): any
-    // candidates give a valid bound, and there a pass-1 sweep costs more than
-    // the extra passers it lets through (c3 select 93 -> 89 us, c5 527 -> 490).
+    // Long rows draw the bound from the first three quarters of the tiles (the
+    // first quarter for d >= 256 on rows of at least 64 tiles, config 5): any
+    // candidates give a valid bound, and the rest of a pass-1 sweep costs more
+    // than the extra passers and drains it lets through (c3 select with pass 1
+    // over 1/2, 3/4, 7/8, all of the row: 86.1, 83.9, 85.1, 87.6 us; c5 527 -> 490
+    // for a quarter against the whole row).
     const int p1 = (NCH * Mfma<T>::KC >= 256 && ntiles >= 64) ? (ntiles + 3) / 4
-                                                              : (ntiles > 16 ? (ntiles + 1) / 2 : ntiles);
+                                                              : (ntiles > 16 ? (3 * ntiles + 3) / 4 : ntiles);
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) L[r] = -INFINITY;
     // MASKED: the tile runs past Nq (only the last one); its extra rows drop out
