@@ -158,10 +158,15 @@ __global__ __launch_bounds__(256, agg_min_blocks<KM>()) void agg_kernel(AggArgs 
     typedef typename Vec<T, VW>::Raw Raw;
     const int step = 256 / LPT;
     if (c0 < dout) {
+      // Unconditional loads (token and neighbour slot clamped into range): the
+      // compiler then knows how many loads follow each group's and waits for
+      // that group alone (a conditional prefetch made every use wait for all
+      // loads, the next group's included, so the gathers did not overlap).
       auto load = [&](int tt, Raw (&raw)[KM]) __attribute__((always_inline)) {
+        const int tc = min(tt, ntok - 1);
 #pragma unroll
         for (int r = 0; r < KM; ++r)
-          if (r < a.K) raw[r] = Vec<T, VW>::raw(V + (uint32_t)(sj[tt * a.K + r] * a.dkp + c0));
+          raw[r] = Vec<T, VW>::raw(V + (uint32_t)(sj[tc * a.K + min(r, a.K - 1)] * a.dkp + c0));
       };
       // merge position of (token i0 + tt, channel c0) and its step per pass
       int tt0 = tid / LPT;
@@ -212,13 +217,13 @@ __global__ __launch_bounds__(256, agg_min_blocks<KM>()) void agg_kernel(AggArgs 
       };
       Raw ra[KM], rb[KM];
       int tt = tt0;
-      if (tt < ntok) load(tt, ra);
+      load(tt, ra);
       // two steps per iteration so the buffers alternate without copies
       for (; tt < ntok; tt += 2 * step) {
-        if (tt + step < ntok) load(tt + step, rb);
+        load(tt + step, rb);
         conv_emit(tt, ra);
         if (tt + step >= ntok) break;
-        if (tt + 2 * step < ntok) load(tt + 2 * step, ra);
+        load(tt + 2 * step, ra);
         conv_emit(tt + step, rb);
       }
     }
