@@ -110,6 +110,11 @@ SELECT_CASES = [
     ("c1_cosine_f32", dict(d_hidden=192, num_heads=3, K=9, magnitude_type="cosine", seq_length=65), 8, 65, torch.float32),
     ("matmul_f32_N197", dict(d_hidden=192, num_heads=3, K=9, seq_length=197), 4, 197, torch.float32),
     ("matmul_bf16_N1024", dict(d_hidden=384, num_heads=3, K=9, seq_length=1024), 2, 1024, torch.bfloat16),
+    # long rows (more than 16 tiles: the pass-1 bound from three quarters of the
+    # row, mid-sweep drains of raw keys into float-key lists) in float32, and
+    # cosine on a row of 19 tiles
+    ("matmul_f32_N1024", dict(d_hidden=192, num_heads=3, K=9, seq_length=1024), 1, 1024, torch.float32),
+    ("cosine_bf16_N600", dict(d_hidden=256, num_heads=2, K=7, magnitude_type="cosine", seq_length=600), 2, 600, torch.bfloat16),
     ("euclid_f32", dict(d_hidden=64, num_heads=2, K=5, magnitude_type="euclidean", seq_length=150), 3, 150, torch.float32),
     ("k16_bf16_d256", dict(d_hidden=768, num_heads=3, K=16, seq_length=300), 1, 300, torch.bfloat16),
     ("k32_f32", dict(d_hidden=32, num_heads=1, K=32, seq_length=90), 2, 90, torch.float32),
