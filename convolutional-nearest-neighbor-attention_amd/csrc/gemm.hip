@@ -21,6 +21,8 @@
 // residual-stream row (W_o + residual, fc2 + residual) also writes those
 // partials for the rows it stores, so the LayerNorm that follows costs no
 // pass of its own.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -235,12 +237,6 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
   // acc[i][j] holds the transposed 32 x 32 block: rows = output columns
   // n0 + wn*64 + j*32 + .., columns = output rows m0 + wm*64 + i*32 + lane%32
   f32x16_t acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
   fetch(0);
   if (XF & 1) {
@@ -279,7 +275,9 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
     __syncthreads();
   }
 
-  for (int k0 = 0; k0 < g.Kd; k0 += BK) {
+  // one k-tile; FIRST: the first one starts the accumulators from zero (a zero
+  // C operand in the MFMA instead of 64 register clears per tile)
+  auto kstep = [&](int k0, auto FIRST) __attribute__((always_inline)) {
     stash(k0);
     __syncthreads();
     if (k0 + BK < g.Kd) fetch(k0 + BK);
@@ -295,9 +293,29 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = M_::mma(bfr[j], af[i], acc[i][j]);
+        for (int j = 0; j < 2; ++j) {
+          if (decltype(FIRST)::value && ks == 0) {
+            f32x16_t z;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) z[v] = 0.0f;
+            acc[i][j] = M_::mma(bfr[j], af[i], z);
+          } else {
+            acc[i][j] = M_::mma(bfr[j], af[i], acc[i][j]);
+          }
+        }
     }
     __syncthreads();
+  };
+  if (g.Kd > 0) {
+    kstep(0, std::true_type{});
+    for (int k0 = BK; k0 < g.Kd; k0 += BK) kstep(k0, std::false_type{});
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
   }
 
   if constexpr (sizeof(T) == 2) if (g.ostage) {
@@ -595,7 +613,8 @@ __global__ __launch_bounds__(256, 2) void gemm_dl_kernel(GemmArgs g) {
   for (int i = 0; i < WI; ++i) {
     const int r = (i * 4 + wave) * RPI + (lane >> 3);
     const int n = min(n0 + r, g.Nc - 1);
-    const int mat = n / g.ncol_each;
+    // at most three stacked matrices: the index by two compares, not a division
+    const int mat = (n >= g.ncol_each ? 1 : 0) + (n >= 2 * g.ncol_each ? 1 : 0);
     wsrc[i] = static_cast<const T*>(g.w[mat]) + (int64_t)(n - mat * g.ncol_each) * g.Kd + chunk(r, lane & 7) * 8;
   }
   auto issue = [&](int buf, int k0) __attribute__((always_inline)) {
@@ -607,14 +626,10 @@ __global__ __launch_bounds__(256, 2) void gemm_dl_kernel(GemmArgs g) {
   };
 
   f32x16_t acc[MI][NJ];
-#pragma unroll
-  for (int i = 0; i < MI; ++i)
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
   const int arow = wm * MI * 32 + (lane & 31), brow = wn * NJ * 32 + (lane & 31);
-  auto compute = [&](int buf) __attribute__((always_inline)) {
+  // FIRST: the first k-tile starts the accumulators from zero (a zero C
+  // operand in the MFMA instead of 96 register clears per tile)
+  auto compute = [&](int buf, auto FIRST) __attribute__((always_inline)) {
     const unsigned char* sp = smem + buf * STAGE;
 #pragma unroll
     for (int ks = 0; ks < BK / M_::KC; ++ks) {
@@ -629,7 +644,16 @@ __global__ __launch_bounds__(256, 2) void gemm_dl_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) acc[i][j] = M_::mma(bfr[j], af[i], acc[i][j]);
+        for (int j = 0; j < NJ; ++j) {
+          if (decltype(FIRST)::value && ks == 0) {
+            f32x16_t z;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) z[v] = 0.0f;
+            acc[i][j] = M_::mma(bfr[j], af[i], z);
+          } else {
+            acc[i][j] = M_::mma(bfr[j], af[i], acc[i][j]);
+          }
+        }
     }
   };
   const int nk = g.Kd / BK;
@@ -638,7 +662,10 @@ __global__ __launch_bounds__(256, 2) void gemm_dl_kernel(GemmArgs g) {
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's loads of tile kt are in LDS
     __syncthreads();                      // ... everyone's; and tile kt - 1 is consumed
     if (kt + 1 < nk) issue((kt + 1) & 1, (kt + 1) * BK);
-    compute(kt & 1);
+    if (kt == 0)
+      compute(0, std::true_type{});
+    else
+      compute(kt & 1, std::false_type{});
   }
   __syncthreads();
 
@@ -691,7 +718,7 @@ __global__ __launch_bounds__(256, 2) void gemm_dl_kernel(GemmArgs g) {
   bool whole = n + 8 <= g.Nc;
   const int mfirst = m0 + tid / SEGS;
   if (OMODE == GEMM_O_HEADSPLIT) {
-    mat = n / g.ncol_each;
+    mat = (n >= g.ncol_each ? 1 : 0) + (n >= 2 * g.ncol_each ? 1 : 0);
     const int nn = n - mat * g.ncol_each;
     hh = nn / g.o_dk;
     cc = nn - hh * g.o_dk;
@@ -768,7 +795,7 @@ int launch_dl(int amode, int omode, const GemmArgs& g, hipStream_t s) {
     return DL_SKIP;
   } else {
     if (amode != GEMM_A_ROWS || !g.ostage || g.ln_stats || g.st_out) return DL_SKIP;
-    if (!g.avec || !g.bvec || g.Kd % DL_BK != 0) return DL_SKIP;
+    if (!g.avec || !g.bvec || g.Kd <= 0 || g.Kd % DL_BK != 0) return DL_SKIP;
     // 16-byte aligned sources for every row (the loads bypass the registers)
     if ((uintptr_t)g.a % 16 != 0 || (g.lda * (int64_t)sizeof(T)) % 16 != 0) return DL_SKIP;
     for (int i = 0; i < 3; ++i)
