@@ -161,6 +161,16 @@ CNNA_DEV float from_lower(float x) {
   return __lane_id() < 32 ? x : __uint_as_float(r[0]);
 }
 
+// c ? t : f as one v_cndmask_b32 on the wave's lane mask of c.  A plain ?: on
+// a value just loaded from LDS can be compiled into an exec-masked branch per
+// select (the load sunk into it); this form stays one VALU instruction.
+CNNA_DEV uint32_t vsel(bool c, uint32_t t, uint32_t f) {
+  const uint64_t m = __builtin_amdgcn_ballot_w64(c);
+  uint32_t r;
+  asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(r) : "v"(f), "v"(t), "s"(m));
+  return r;
+}
+
 // Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), every lane gets
 // it; no LDS traffic.  All 16 lanes must be active.
 template <int CTRL>

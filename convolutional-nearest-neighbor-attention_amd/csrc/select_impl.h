@@ -94,9 +94,14 @@ CNNA_DEV void list_insert(uint64_t (&L)[KMAX], uint64_t x) {
   L[0] = b[0] ? x : L[0];
 }
 
-// max(a, b) for non-NaN inputs as one v_med3_f32 (fmaxf would first
-// canonicalise both operands, two more VALU ops)
-CNNA_DEV float max2(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, INFINITY); }
+// max(a, b) for non-NaN inputs as one VALU op (fmaxf, and a med3 against
+// +inf, which the compiler turns into fmaxf, first canonicalise both operands:
+// two more VALU ops)
+CNNA_DEV float max2(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 // max of three non-NaN floats, one VALU op
 CNNA_DEV float max3(float a, float b, float c) {
   float r;
@@ -467,10 +472,10 @@ void select_kernel(SelArgs a) {
 #pragma unroll
           for (int r = KMAX - 1; r >= 1; --r) {
             Lk[r] = __builtin_amdgcn_fmed3f(Lk[r - 1], xk, Lk[r]);
-            Li[r] = b[r - 1] ? Li[r - 1] : (b[r] ? xi : Li[r]);
+            Li[r] = vsel(b[r], vsel(b[r - 1], Li[r - 1], xi), Li[r]);   // b[r-1] implies b[r]
           }
           Lk[0] = b[0] ? xk : Lk[0];
-          Li[0] = b[0] ? xi : Li[0];
+          Li[0] = vsel(b[0], xi, Li[0]);
         }
 #pragma unroll
         for (int r = 0; r < KMAX; ++r) L2[r] = Lk[r] == -INFINITY ? 0 : pack_entry(Lk[r], Li[r]);
