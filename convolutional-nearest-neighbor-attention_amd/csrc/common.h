@@ -132,17 +132,25 @@ template <> struct Mfma<float> {
 // nn.GELU() (erf form): 0.5 x (1 + erf(x / sqrt 2)) with erf from Abramowitz &
 // Stegun, Handbook of Mathematical Functions (1964), formula 7.1.26:
 //   erfc(z) = (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),  t = 1 / (1 + p z),
-// absolute error <= 1.5e-7 for z >= 0.  For x < 0 the factor 1 + erf is erfc(|z|)
-// itself (no cancellation).  About a dozen VALU operations.
+// absolute error <= 1.5e-7 for z >= 0.  Written as
+//   gelu(x) = max(x, 0) - |x| h,  h = Phi(-|x|) = erfc(|x| / sqrt 2) / 2,
+// which holds for either sign and needs no cancellation-prone 1 - h: the
+// 1 / sqrt 2 goes into p, the 1/2 into the a_i, and exp(-x^2 / 2) is
+// exp2(-x^2 log2(e) / 2).  Thirteen VALU operations, two of them
+// transcendental; +inf is passed through (the product would be inf * 0), -inf
+// and NaN give NaN as the erf form does.
 CNNA_DEV float gelu_erf(float x) {
-  const float z = fabsf(x) * 0.70710678118654752f;
-  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, z, 1.0f));
-  float p = __builtin_fmaf(1.061405429f, t, -1.453152027f);
-  p = __builtin_fmaf(p, t, 1.421413741f);
-  p = __builtin_fmaf(p, t, -0.284496736f);
-  p = __builtin_fmaf(p, t, 0.254829592f);
-  const float erfc = p * t * __expf(-z * z);
-  return 0.5f * x * (x >= 0.0f ? 2.0f - erfc : erfc);
+  const float ax = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f * 0.70710678118654752f, ax, 1.0f));
+  float p = __builtin_fmaf(0.5f * 1.061405429f, t, 0.5f * -1.453152027f);
+  p = __builtin_fmaf(p, t, 0.5f * 1.421413741f);
+  p = __builtin_fmaf(p, t, 0.5f * -0.284496736f);
+  p = __builtin_fmaf(p, t, 0.5f * 0.254829592f);
+  const float e = __builtin_amdgcn_exp2f(x * (x * -0.72134752044448170f));
+  float pos;   // max(x, 0) without the operand canonicalisation fmaxf adds
+  asm("v_max_f32 %0, 0, %1" : "=v"(pos) : "v"(x));
+  const float g = __builtin_fmaf(-ax, (p * t) * e, pos);
+  return x == INFINITY ? x : g;
 }
 
 // The value of lane l ^ 32 (the other half of the wave) without a trip through
