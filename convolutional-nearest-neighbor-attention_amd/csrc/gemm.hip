@@ -280,6 +280,10 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
   auto kstep = [&](int k0, auto FIRST) __attribute__((always_inline)) {
     stash(k0);
     __syncthreads();
+    // the next tile's loads and the MFMA loop at a raised wave priority, ahead
+    // of the other blocks' prologue / epilogue VALU work on the SIMD (ViT
+    // forward about 1.5 % faster; the direct-to-LDS kernel measured no gain)
+    __builtin_amdgcn_s_setprio(1);
     if (k0 + BK < g.Kd) fetch(k0 + BK);
 #pragma unroll
     for (int ks = 0; ks < BK / M_::KC; ++ks) {
@@ -304,6 +308,7 @@ __global__ __launch_bounds__(256, 3) void gemm_kernel(GemmArgs g) {
           }
         }
     }
+    __builtin_amdgcn_s_setprio(0);
     __syncthreads();
   };
   if (g.Kd > 0) {

@@ -231,6 +231,8 @@ __global__ __launch_bounds__(256) void gemm_grad_kernel(GradGemmArgs g) {
     OA::stash(ra, As, tid);
     OW::stash(rw, Bs, tid);
     __syncthreads();
+    // next tile's loads and the MFMA loop at a raised wave priority
+    __builtin_amdgcn_s_setprio(1);
     if (k0 + BK < kend) {
       OA::fetch(ra, abase, 0, g.lda, g.avec, g.M, m0, k0 + BK, kend, tid, ga);
       OW::fetch(rw, wbase, g.w_krows, g.ldw, g.bvec, g.Nc, n0, k0 + BK, kend, tid, ga, GI ? &ix : nullptr,
@@ -253,6 +255,7 @@ __global__ __launch_bounds__(256) void gemm_grad_kernel(GradGemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = M_::mma(bfr[j], af[i], acc[i][j]);
     }
+    __builtin_amdgcn_s_setprio(0);
     __syncthreads();
   }
 

@@ -246,6 +246,7 @@ void select_kernel(SelArgs a) {
     u32x4_t (&pf)[NPF] = pfs[decltype(SLOT)::value];
     float& pfn = pfns[decltype(SLOT)::value];
     int& pfc = pfcs[decltype(SLOT)::value];
+    __builtin_amdgcn_s_setprio(2);
     const int j0 = tile * TJ;
 #pragma unroll
     for (int i = 0; i < NPF; ++i) {
@@ -255,6 +256,7 @@ void select_kernel(SelArgs a) {
       r = min(j0 + min(r, TJ - 1), a.Nq - 1);
       pf[i] = *reinterpret_cast<const u32x4_t*>(Qb + (int64_t)r * dkp + cv * VEC);
     }
+    __builtin_amdgcn_s_setprio(0);
     if (EUC || SMP) {
       const int j = min(j0 + (tid & (TJ - 1)), a.Nq - 1);
       if (EUC) pfn = a.qn[(int64_t)bh * a.Nq + j];
@@ -285,6 +287,10 @@ void select_kernel(SelArgs a) {
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
+    // the MFMA chain (and below, the next tile's global loads) is issued at a
+    // raised wave priority, ahead of the other waves' filter work on the SIMD,
+    // so the matrix core starts sooner (c3 select about 2 % faster)
+    __builtin_amdgcn_s_setprio(2);
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       if (EXACT || c < nch) {
@@ -295,6 +301,7 @@ void select_kernel(SelArgs a) {
         for (int b = 0; b < NB; ++b) acc[b] = M_::mma(af[b], kf[c], acc[b]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
   };
   // ranking key of one accumulator entry
   auto keyof = [&](float accv, int buf, int jl) __attribute__((always_inline)) -> float {
