@@ -78,6 +78,36 @@ def test_linear_epilogues(dtype, M, Nout, Kd, mode):
         torch.testing.assert_close(out.float(), ref.float(), rtol=2e-2, atol=2e-2)
 
 
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_linear_gelu_values(dtype):
+    """The GELU epilogue as a function: with A = 0 the GEMM output is the bias,
+    so every column checks GELU at one input (a sweep over [-20, 20], values
+    near 0 and the special values) against nn.GELU's erf form in float64.
+    Bounds: the erf approximation's 1.5e-7 plus float32 rounding; in bf16 one
+    rounding of the same value (an ulp apart where it falls near a tie)."""
+    sweep = torch.linspace(-20.0, 20.0, 4000, dtype=torch.float64)
+    small = torch.tensor([0.0, -0.0, 1e-30, -1e-30, 1e-7, -1e-7, 3e-3, -3e-3], dtype=torch.float64)
+    special = torch.tensor([float("inf"), float("-inf"), float("nan"), 3e38, -3e38], dtype=torch.float64)
+    xs = torch.cat([sweep, small, special]).to(dtype)
+    n = ((xs.numel() + 7) // 8) * 8
+    bias = torch.cat([xs, torch.zeros(n - xs.numel(), dtype=dtype)]).to(DEV)
+    a = torch.zeros(64, 64, device=DEV, dtype=dtype)
+    W = torch.zeros(n, 64, device=DEV, dtype=dtype)
+    out = ops.linear(a, W, bias, gelu=True)
+    ref = F.gelu(bias.double())                    # erf form, float64
+    for row in (0, 63):
+        got = out[row].double()
+        fin = torch.isfinite(ref)
+        # the special values: +inf -> +inf, -inf and NaN -> NaN, as the erf form gives
+        assert torch.equal(torch.isnan(got), torch.isnan(ref))
+        assert torch.equal(got[torch.isinf(ref)], ref[torch.isinf(ref)])
+        if dtype == torch.float32:
+            torch.testing.assert_close(got[fin], ref[fin], rtol=1e-6, atol=1e-6)
+        else:
+            torch.testing.assert_close(got[fin], ref[fin].to(dtype).double(), rtol=8e-3, atol=1e-6)
+
+
 def _tiny_vit(dtype):
     torch.manual_seed(0)
     args = vit_tiny_args(img_size=(3, 64, 64), patch_size=8, num_layers=3, dropout=0.0,
