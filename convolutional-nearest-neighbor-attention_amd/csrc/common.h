@@ -136,9 +136,10 @@ template <> struct Mfma<float> {
 //   gelu(x) = max(x, 0) - |x| h,  h = Phi(-|x|) = erfc(|x| / sqrt 2) / 2,
 // which holds for either sign and needs no cancellation-prone 1 - h: the
 // 1 / sqrt 2 goes into p, the 1/2 into the a_i, and exp(-x^2 / 2) is
-// exp2(-x^2 log2(e) / 2).  Thirteen VALU operations, two of them
-// transcendental; +inf is passed through (the product would be inf * 0), -inf
-// and NaN give NaN as the erf form does.
+// exp2(-x^2 log2(e) / 2).  Fifteen VALU operations as compiled, two of them
+// transcendental (eighteen for 0.5 x (2 - erfc) or 0.5 x erfc by sign); +inf
+// is passed through (the product would be inf * 0), -inf and NaN give NaN as
+// the erf form does.
 CNNA_DEV float gelu_erf(float x) {
   const float ax = fabsf(x);
   const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f * 0.70710678118654752f, ax, 1.0f));
